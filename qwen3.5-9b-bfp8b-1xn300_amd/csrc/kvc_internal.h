@@ -1,0 +1,160 @@
+// kvc_internal.h -- shapes, device layouts and kernel-argument blocks shared by
+// the host bookkeeping (kvc_host.cpp) and the gfx950 kernels (*.hip).
+//
+// HBM layout of the K/V pools (one allocation per context):
+//   pool[layer][kv(0=K,1=V)][block][kv_head][tok(32)][d(256)]   bf16
+// so a (block, kv_head) unit is 32*256*2 = 16 KiB contiguous and a block of one
+// layer is 64 KiB.  Block ids are shared by all attention layers: a sequence's
+// block table maps token position p -> block table[p / 32], slot p % 32, in
+// every layer's pool.  The reference keeps one contiguous fp32 array per layer
+// instead (src/engine.cpp:81-84, index pos*kv_dim + kv_h*D + d at :3539).
+//
+// Recurrent state of a sequence slot (one contiguous region per slot):
+//   [ssm_layer][ rec fp32 [v_heads][v_dim][k_dim] | conv fp32 [rows][channels] ]
+// matching g_ssm_state / g_conv_state (src/engine.cpp:86-94, :3840-3843).
+//
+// Snapshot slot (one contiguous region per slot):
+//   [ state of one sequence (as above) | kv segment [layer][kv][seg_blocks][64 KiB] ]
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace kvc {
+
+// Kernel specialisation: Qwen3.5 full-attention shapes (model_config.h:15-17).
+constexpr int kHeadDim = 256;
+constexpr int kKvHeads = 4;
+constexpr int kGroup = 4;  // q heads per kv head (16 / 4)
+constexpr int kQHeads = kKvHeads * kGroup;
+constexpr int kBlockTok = 32;
+constexpr size_t kUnitBytes = (size_t)kBlockTok * kHeadDim * 2;  // 16 KiB
+constexpr size_t kBlockBytes = kUnitBytes * kKvHeads;            // 64 KiB
+
+constexpr int kMaxBatch = 64;        // seqs per kernel launch (argument block)
+constexpr int kMaxChunks = 8192;     // split-K work chunks per decode launch
+constexpr int kTableUpdatesPerLaunch = 480;
+
+// ---- kernel argument blocks (passed by value; must stay < 4 KiB) ----------
+
+struct TableUpdateArgs {
+    int32_t* table;   // device block table [max_seqs][max_blocks]
+    int32_t n;
+    int32_t pad;
+    int32_t index[kTableUpdatesPerLaunch];  // slot * max_blocks + block index
+    int32_t block[kTableUpdatesPerLaunch];
+};
+
+struct DecodeArgs {
+    const uint16_t* kpool;  // this layer's K pool base
+    const uint16_t* vpool;
+    const int32_t* table;
+    const uint16_t* q;      // [n_seqs][Hq][D]
+    const uint16_t* k_new;  // [n_seqs][Hkv][D] or null
+    const uint16_t* v_new;
+    const uint16_t* gate;   // [n_seqs][Hq][D] or null
+    void* out;              // [n_seqs][Hq][D]
+    float* part;            // split-K workspace [item][G][D + 2]
+    int32_t* counters;      // [kMaxBatch][Hkv] arrival counters (self-resetting)
+    float scale_log2;       // scale * log2(e)
+    int32_t out_bf16;
+    int32_t table_stride;   // max blocks per seq
+    int32_t n_seqs;
+    int32_t chunk_blocks;   // blocks per split-K chunk
+    int32_t total_chunks;   // sum over seqs
+    int32_t n_items;        // total_chunks * Hkv
+    int32_t per_xcd;        // ceil(n_items / 8)
+    int32_t slot[kMaxBatch];
+    int32_t kv_len[kMaxBatch];       // keys attended (new token included)
+    int32_t chunk_begin[kMaxBatch + 1];
+};
+
+struct AppendArgs {
+    uint16_t* kpool;
+    uint16_t* vpool;
+    const int32_t* table;
+    const uint16_t* k;  // [n_seqs][n_tok][Hkv][D]
+    const uint16_t* v;
+    int32_t table_stride;
+    int32_t n_seqs;
+    int32_t n_tok;
+    int32_t pad;
+    int32_t slot[kMaxBatch];
+    int32_t pos0[kMaxBatch];  // first position written
+};
+
+struct GatherArgs {
+    const uint16_t* kpool;
+    const uint16_t* vpool;
+    const int32_t* table;
+    uint16_t* k_out;
+    uint16_t* v_out;
+    int32_t table_stride;
+    int32_t n_seqs;
+    int32_t tok0;
+    int32_t total_tok;
+    int32_t slot[kMaxBatch];
+    int32_t out_begin[kMaxBatch + 1];  // token offsets into the packed output
+};
+
+struct PrefillArgs {
+    const uint16_t* kpool;
+    const uint16_t* vpool;
+    const int32_t* table;
+    const uint16_t* q;     // [n_seqs][n_q][Hq][D]
+    const uint16_t* gate;  // same or null
+    void* out;
+    float scale_log2;
+    int32_t out_bf16;
+    int32_t table_stride;
+    int32_t n_seqs;
+    int32_t n_q;
+    int32_t pad;
+    int32_t slot[kMaxBatch];
+    int32_t q_pos0[kMaxBatch];  // position of query row 0
+};
+
+// Snapshot copy: per pair, state bytes then the K/V segment.
+struct SnapshotArgs {
+    uint8_t* state_base;     // live state pool
+    uint8_t* snap_base;      // snapshot pool
+    uint8_t* pool_base;      // K/V pools (all layers)
+    const int32_t* table;
+    int64_t state_bytes;     // per sequence slot
+    int64_t snap_bytes;      // per snapshot slot
+    int64_t layer_kv_bytes;  // bytes of one (layer, kv) pool = n_blocks * 64 KiB
+    int32_t n_layers;        // attention layers
+    int32_t seg_blocks;      // blocks per segment
+    int32_t table_stride;
+    int32_t restore;         // 0 = save (live -> snap), 1 = restore
+    int32_t n_pairs;
+    int32_t do_state;        // copy the recurrent state part
+    int32_t do_kv;           // copy the K/V segment part
+    int32_t pad;
+    int32_t seq_slot[kMaxBatch];
+    int32_t snap_slot[kMaxBatch];
+    int32_t first_block[kMaxBatch];  // block-table index of the segment start
+};
+
+// Copy whole blocks (all layers, K and V): copy-on-write of a shared block.
+struct BlockCopyArgs {
+    uint8_t* pool_base;
+    int64_t layer_kv_bytes;
+    int32_t n_layers;
+    int32_t n;
+    int32_t src[kMaxBatch];
+    int32_t dst[kMaxBatch];
+};
+
+// ---- launchers (kvc_kernels.hip); return hipError_t as int ---------------
+int launch_table_update(const TableUpdateArgs& a, void* stream);
+int launch_decode(const DecodeArgs& a, void* stream);
+int launch_append(const AppendArgs& a, int n_units, void* stream);
+int launch_gather(const GatherArgs& a, void* stream);
+int launch_prefill(const PrefillArgs& a, void* stream);
+int launch_snapshot(const SnapshotArgs& a, void* stream);
+int launch_block_copy(const BlockCopyArgs& a, void* stream);
+int launch_fill_normal(uint16_t* dst, int64_t n, uint64_t seed, float scale,
+                       void* stream);
+
+}  // namespace kvc

@@ -1,0 +1,180 @@
+"""ctypes binding of oracle/libkvc_oracle.so (test infrastructure) and the
+independent fp64 checks that pin it.
+
+Only tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_DIR = ROOT / "oracle"
+ORACLE_LIB = ORACLE_DIR / "libkvc_oracle.so"
+
+_L = None
+
+
+def build_oracle():
+    subprocess.run(["make", "-C", str(ORACLE_DIR)], check=True, capture_output=True)
+
+
+def L() -> ctypes.CDLL:
+    global _L
+    if _L is None:
+        if not ORACLE_LIB.exists():
+            build_oracle()
+        lib = ctypes.CDLL(str(ORACLE_LIB))
+        P = ctypes.c_void_p
+        I = ctypes.c_int
+        F = ctypes.c_float
+        U64 = ctypes.c_uint64
+        sigs = {
+            "orc_splitmix64_next": (U64, [ctypes.POINTER(U64)]),
+            "orc_splitmix64_at": (U64, [U64, U64]),
+            "orc_box_muller": (None, [U64, ctypes.POINTER(F), ctypes.POINTER(F)]),
+            "orc_fill_normal_bf16": (None, [P, ctypes.c_size_t, U64, F]),
+            "orc_fill_normal_f32": (None, [P, ctypes.c_size_t, U64, F]),
+            "orc_f32_to_bf16_rne": (ctypes.c_uint16, [F]),
+            "orc_f32_to_bf16_trunc": (ctypes.c_uint16, [F]),
+            "orc_bf16_to_f32": (F, [ctypes.c_uint16]),
+            "orc_f32_to_bf16_rne_n": (None, [P, P, ctypes.c_size_t]),
+            "orc_bf16_to_f32_n": (None, [P, P, ctypes.c_size_t]),
+            "orc_fast_expf": (F, [F]),
+            "orc_sigmoid": (F, [F, I]),
+            "orc_cache_append": (None, [P, P, I, I, I, I, P, P]),
+            "orc_cache_gather": (None, [P, P, I, I, I, I, P, P]),
+            "orc_decode_attn": (None, [P, P, P, I, I, I, I, F, P, I, P]),
+            "orc_prefill_attn": (None, [P, P, P, I, I, I, I, I, F, P, I, P]),
+            "orc_decode_attn_batch": (None, [I, P, P, P, P, I, I, I, F, P, I]),
+            "orc_max_threads": (I, []),
+            "orc_truncate_count": (I, [I, I, I]),
+            "orc_reference_prefix": (I, [P, I, P, I, ctypes.POINTER(I)]),
+            "orc_lcp": (I, [P, I, P, I]),
+            "orc_block_hash": (U64, [U64, P, I, I]),
+            "orc_hash_root": (U64, []),
+            "orc_hash_chain": (None, [P, I, I, I, P]),
+            "orc_reuse_len": (I, [I, I, I, I, P, I, I]),
+            "orc_conv_push": (None, [P, I, I, P]),
+            "orc_deltanet_head_step": (None, [P, I, I, P, P, P, F, F, F, P]),
+        }
+        for n, (r, a) in sigs.items():
+            f = getattr(lib, n)
+            f.restype = r
+            f.argtypes = a
+        _L = lib
+    return _L
+
+
+def _p(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+# ---- bf16 helpers (numpy) ------------------------------------------------
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    L().orc_f32_to_bf16_rne_n(_p(x), _p(out), x.size)
+    return out
+
+
+def normal_bf16(n: int, seed: int, scale: float = 1.0) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    L().orc_fill_normal_bf16(_p(out), n, seed, scale)
+    return out
+
+
+# ---- oracle wrappers -------------------------------------------------------
+
+def decode_attn(q, kc, vc, L_, n_q=16, n_kv=4, d=256, scale=1 / 16, gate=None, gate_mode=0):
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    kc = np.ascontiguousarray(kc, dtype=np.uint16)
+    vc = np.ascontiguousarray(vc, dtype=np.uint16)
+    g = None if gate is None else np.ascontiguousarray(gate, dtype=np.uint16)
+    out = np.empty((n_q, d), dtype=np.float32)
+    L().orc_decode_attn(_p(q), _p(kc), _p(vc), L_, n_q, n_kv, d, scale, _p(g), gate_mode, _p(out))
+    return out
+
+
+def prefill_attn(q, kc, vc, pos0, n, n_q=16, n_kv=4, d=256, scale=1 / 16, gate=None, gate_mode=0):
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    kc = np.ascontiguousarray(kc, dtype=np.uint16)
+    vc = np.ascontiguousarray(vc, dtype=np.uint16)
+    g = None if gate is None else np.ascontiguousarray(gate, dtype=np.uint16)
+    out = np.empty((n, n_q, d), dtype=np.float32)
+    L().orc_prefill_attn(_p(q), _p(kc), _p(vc), pos0, n, n_q, n_kv, d, scale, _p(g), gate_mode, _p(out))
+    return out
+
+
+def decode_attn_batch(q, kcs, vcs, Ls, n_q=16, n_kv=4, d=256, scale=1 / 16, threads=0):
+    n = len(kcs)
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    kp = (ctypes.c_void_p * n)(*[k.ctypes.data for k in kcs])
+    vp = (ctypes.c_void_p * n)(*[v.ctypes.data for v in vcs])
+    Larr = (ctypes.c_int * n)(*Ls)
+    out = np.empty((n, n_q, d), dtype=np.float32)
+    L().orc_decode_attn_batch(n, _p(q), ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p),
+                              ctypes.cast(Larr, ctypes.c_void_p), n_q, n_kv, d, scale, _p(out), threads)
+    return out
+
+
+def reference_prefix(cached, prompt):
+    c = np.ascontiguousarray(cached, dtype=np.int32)
+    p = np.ascontiguousarray(prompt, dtype=np.int32)
+    reset = ctypes.c_int()
+    n = L().orc_reference_prefix(_p(c), len(c), _p(p), len(p), ctypes.byref(reset))
+    return n, bool(reset.value)
+
+
+def hash_chain(tok, n_blocks, block=32, weak=False):
+    t = np.ascontiguousarray(tok, dtype=np.int32)
+    out = np.empty(n_blocks, dtype=np.uint64)
+    L().orc_hash_chain(_p(t), n_blocks, block, int(weak), _p(out))
+    return out
+
+
+def reuse_len(lcp, n_prompt, block, interval, snap, has_ssm):
+    s = np.ascontiguousarray(snap, dtype=np.uint8)
+    return L().orc_reuse_len(lcp, n_prompt, block, interval, _p(s) if len(s) else None, len(s), int(has_ssm))
+
+
+# ---- independent fp64 brute force (the pin) ------------------------------
+
+def attn_fp64(q_bf16, k_bf16, v_bf16, scale, n_q=16, n_kv=4, gate_bf16=None):
+    """Exact two-pass softmax in float64: out[h] = sum_j softmax(s)_j v_j with
+    s_j = scale * q_h . k_j for keys of kv head h // (n_q // n_kv)."""
+    q = bf16_to_f32(q_bf16).astype(np.float64).reshape(n_q, -1)
+    d = q.shape[1]
+    k = bf16_to_f32(k_bf16).astype(np.float64).reshape(-1, n_kv, d)
+    v = bf16_to_f32(v_bf16).astype(np.float64).reshape(-1, n_kv, d)
+    out = np.empty((n_q, d))
+    grp = n_q // n_kv
+    for h in range(n_q):
+        kh = k[:, h // grp, :]
+        vh = v[:, h // grp, :]
+        s = kh @ q[h] * scale
+        w = np.exp(s - s.max())
+        out[h] = (w[:, None] * vh).sum(0) / w.sum()
+    if gate_bf16 is not None:
+        g = bf16_to_f32(gate_bf16).astype(np.float64).reshape(n_q, d)
+        out *= 1.0 / (1.0 + np.exp(-g))
+    return out
+
+
+def assert_attn_close(got, want, atol=2e-2, rel_rms=1e-2, what=""):
+    """Attention tolerance: max |diff| <= atol AND rms(diff)/rms(want) <= rel_rms."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    diff = got - want
+    mx = float(np.abs(diff).max()) if diff.size else 0.0
+    rr = float(np.sqrt((diff ** 2).mean()) / max(np.sqrt((want ** 2).mean()), 1e-30)) if diff.size else 0.0
+    assert mx <= atol and rr <= rel_rms, f"{what}: max|diff|={mx:.3e} (atol {atol}), rel rms={rr:.3e} (<= {rel_rms})"
+    return mx, rr

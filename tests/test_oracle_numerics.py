@@ -1,0 +1,111 @@
+"""Pins the oracle's numeric helpers: generator, bf16 rounding, Schraudolph exp.
+
+Each check is fixed by something other than the oracle's own formula: a
+published test vector, exhaustive comparison with exact fp64 nearest-even
+rounding, or closed forms.
+"""
+import ctypes
+import math
+
+import numpy as np
+
+import _oracle as O
+
+
+def test_splitmix64_published_vector():
+    # Vigna's splitmix64 reference output for seed 1234567
+    s = ctypes.c_uint64(1234567)
+    got = [O.L().orc_splitmix64_next(ctypes.byref(s)) for _ in range(5)]
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                   4593380528125082431, 16408922859458223821]
+    # the counter form returns the same stream
+    assert [O.L().orc_splitmix64_at(1234567, i) for i in range(5)] == got
+
+
+def test_box_muller_closed_form():
+    # draw with top 24 bits = 2^23 - 1 -> u1 = 2^23/2^24 = 0.5, u2 bits = 2^22 -> u2 = 0.25
+    draw = ((2**23 - 1) << 40) | ((2**22) << 16)
+    z0, z1 = ctypes.c_float(), ctypes.c_float()
+    O.L().orc_box_muller(draw, ctypes.byref(z0), ctypes.byref(z1))
+    r = math.sqrt(-2 * math.log(0.5))
+    assert abs(z0.value - r * math.cos(math.pi / 2)) < 1e-6
+    assert abs(z1.value - r * math.sin(math.pi / 2)) < 1e-6
+
+
+def test_normal_fill_moments():
+    x = np.empty(1 << 20, dtype=np.float32)
+    O.L().orc_fill_normal_f32(x.ctypes.data, x.size, 20261202, 1.0)
+    assert abs(x.mean()) < 5e-3
+    assert abs(x.var() - 1.0) < 1e-2
+    assert abs(np.mean(x ** 4) - 3.0) < 5e-2  # Gaussian kurtosis
+    # bf16 fill equals RNE of the f32 fill
+    b = O.normal_bf16(4096, 20261202)
+    assert np.array_equal(b, O.f32_to_bf16(x[:4096]))
+
+
+def _rne_exact(x32: np.ndarray) -> np.ndarray:
+    """Nearest bf16 by exact fp64 distance, ties to even mantissa (finite x)."""
+    u = x32.view(np.uint32)
+    lo = (u >> 16).astype(np.uint32)
+    hi = lo + 1
+
+    def val(b):  # value of a positive bf16 pattern in fp64; 0x7F80 -> 2^128,
+        e = ((b >> 7) & 0xFF).astype(np.int64)  # the rounding neighbour of
+        m = (b & 0x7F).astype(np.float64)        # the largest finite value
+        return np.where(e == 0, m / 128 * 2.0 ** -126, (1 + m / 128) * np.exp2(e - 127.0))
+
+    flo, fhi = val(lo), val(hi)
+    fx = x32.astype(np.float64)
+    dlo, dhi = np.abs(fx - flo), np.abs(fhi - fx)
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & ((lo & 1) == 1))
+    return np.where(pick_hi, hi, lo).astype(np.uint16)
+
+
+def test_bf16_rne_exhaustive_neighbourhoods():
+    # every finite positive bf16 value b (exponent < 0xFF) with low halves
+    # 0, 1, 0x7FFF, 0x8000 (tie), 0x8001, 0xFFFF; plus negatives
+    b = np.arange(0, 0x7F7F + 1, dtype=np.uint32)
+    lows = np.array([0, 1, 0x3FFF, 0x7FFF, 0x8000, 0x8001, 0xC000, 0xFFFF], dtype=np.uint32)
+    u = ((b[:, None] << 16) | lows[None, :]).ravel()
+    u = np.concatenate([u, u | 0x80000000])
+    x = u.view(np.float32)
+    got = O.f32_to_bf16(x)
+    want = _rne_exact(np.abs(x)) | ((u >> 16) & 0x8000).astype(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_bf16_special_values():
+    f = O.L().orc_f32_to_bf16_rne
+    assert f(float("inf")) == 0x7F80
+    assert f(float("-inf")) == 0xFF80
+    n = f(float("nan"))
+    assert (n & 0x7F80) == 0x7F80 and (n & 0x7F) != 0
+    # largest finite float rounds up to +inf (RNE overflow)
+    big = np.array([0x7F7FFFFF], dtype=np.uint32).view(np.float32)[0]
+    assert f(float(big)) == 0x7F80
+    # truncation keeps the top 16 bits (src/engine.cpp:248-252)
+    for v in (1.0, -2.5, 3.14159, 1e-30):
+        u = np.array([v], dtype=np.float32).view(np.uint32)[0]
+        assert O.L().orc_f32_to_bf16_trunc(v) == (u >> 16)
+        assert O.L().orc_bf16_to_f32(int(u >> 16)) == np.array([u & 0xFFFF0000], dtype=np.uint32).view(np.float32)[0]
+
+
+def test_schraudolph_exp():
+    fe = O.L().orc_fast_expf
+    # exact at 0 by construction: bias 127 << 23 is the bit pattern of 1.0
+    assert fe(0.0) == 1.0
+    # slope 2^23 / ln 2: exp(k ln2) lands within the method's error of 2^k
+    for k in range(-10, 11):
+        assert abs(fe(k * math.log(2)) / 2.0 ** k - 1) < 1e-3
+    # clamp to [-88, 88]
+    assert fe(1000.0) == fe(88.0)
+    assert fe(-1000.0) == fe(-88.0)
+    # documented max relative error ~1.7% (src/engine.cpp:2346-2348); the
+    # truncating int conversion gives at most ~6.1% below the true value
+    xs = np.linspace(-20, 20, 4001)
+    err = max(abs(fe(float(x)) / math.exp(x) - 1) for x in xs)
+    assert err < 0.065
+    sig = O.L().orc_sigmoid
+    for x in (-8.0, -1.0, 0.0, 0.5, 3.0):
+        assert abs(sig(x, 0) - 1 / (1 + math.exp(-x))) < 1e-6
+        assert abs(sig(x, 1) - 1 / (1 + math.exp(-x))) < 2e-2
