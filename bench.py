@@ -1,0 +1,552 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X KV-cache path (libkvc.so) on one GPU.
+
+Default workload ("b"): single-sequence decode step,
+8 full-attention layers, 16 q / 4 kv heads, head_dim 256, bf16 cache at 4096
+tokens; per layer one token is appended (fused into the attention launch) and
+GQA decode attention runs over the 4096 keys.  One step = the 8 layer launches,
+replayed from a HIP graph.  Four independent cache replicas (512 MiB) rotate
+step to step so the 256 MB Infinity Cache cannot serve the K/V.  The sequence
+is cut back to 4095 tokens after each step so every step attends over 4096.
+
+Prints one JSON line.  value = algorithmic HBM GB/s of the decode path
+(bytes per layer / measured time per layer).  roofline.achieved uses the
+decode kernel's own average duration from HIP events around each launch; the
+CPU baseline is the oracle (this repository's C restatement of the reference's
+host attention loop) timed on a bounded sample on this host.
+
+Other workloads: --config c|d|e|a print their own line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "qwen3.5-9b-bfp8b-1xn300_amd"))
+
+HBM_PEAK_GBS = 8000.0
+NQ, NKV, D, BT = 16, 4, 256, 32
+ROW = NKV * D
+SEED = 20261201
+METRIC = "KV path HBM GB/s (% of 8 TB/s) + µs/layer decode attn at 4K ctx, 1 GPU"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def host_cores() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------------
+# config b: single-sequence decode at 4K
+
+def bytes_per_layer_b(L=4096):
+    # K/V of L tokens + q + out (bf16) + append read/write of one token
+    return L * ROW * 2 * 2 + NQ * D * 2 + NQ * D * 2 + 2 * ROW * 2 * 2
+
+
+def cpu_baseline_b(L=4096, budget_s=12.0):
+    """Oracle decode (fp32, libm expf) over one layer at L keys; 1 thread and
+    all cores (parallel over the 16 q heads)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import _oracle as O
+
+    k = O.normal_bf16(L * ROW, SEED + 2)
+    v = O.normal_bf16(L * ROW, SEED + 3)
+    q = O.normal_bf16(NQ * D, SEED + 4)
+    res = {}
+    cores = host_cores()
+    for threads in (1, cores):
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            O.decode_attn_batch(q, [k], [v], [L], threads=threads)
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt > budget_s / 2 or n >= 2000:
+                break
+        us = dt / n * 1e6
+        res[threads] = (us, n)
+    return res, cores
+
+
+def run_b(args):
+    import kvc
+
+    h = kvc.hip()
+    if h.device_count() < 1:
+        raise RuntimeError("no HIP device visible")
+    L, layers, reps = 4096, 8, args.replicas
+    blocks_per_seq = L // BT
+    ctx = kvc.Context(n_attn_layers=layers, n_ssm_layers=0, max_seqs=max(reps, 4), max_seq_len=L + 64,
+                      pool_blocks=reps * (blocks_per_seq + 2), snapshot_slots=0, alloc_seed=SEED + 2,
+                      decode_chunk_blocks=args.chunk_blocks)
+    stream = h.stream()
+    log(f"config b: {layers} layers, L={L}, {reps} replicas, pool fill")
+    ctx.pool_fill_normal(SEED + 2, stream)
+    seqs = [ctx.seq_create() for _ in range(reps)]
+    ctx.reserve(seqs, L - 1, stream)
+    ctx.commit(seqs, L - 1, None, stream)
+    q = h.malloc(reps * layers * NQ * D * 2)
+    kn = h.malloc(reps * layers * ROW * 2)
+    vn = h.malloc(reps * layers * ROW * 2)
+    out = h.malloc(reps * layers * NQ * D * 2)
+    ctx.fill_normal_bf16(q, reps * layers * NQ * D, SEED + 4, 1.0, stream)
+    ctx.fill_normal_bf16(kn, reps * layers * ROW, SEED + 5, 1.0, stream)
+    ctx.fill_normal_bf16(vn, reps * layers * ROW, SEED + 6, 1.0, stream)
+    h.stream_sync(stream)
+
+    def enqueue_step(r):
+        for layer in range(layers):
+            i = r * layers + layer
+            ctx.decode_attn(layer, [seqs[r]], q.ptr + i * NQ * D * 2, out.ptr + i * NQ * D * 2,
+                            k_new=kn.ptr + i * ROW * 2, v_new=vn.ptr + i * ROW * 2,
+                            out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
+
+    # one graph per replica (kernel arguments carry the sequence's length)
+    graphs = []
+    for r in range(reps):
+        ctx.reserve([seqs[r]], 1, stream)
+        graphs.append(h.capture(stream, lambda r=r: enqueue_step(r)))
+        ctx.commit([seqs[r]], 1, None, stream)
+        ctx.seq_truncate(seqs[r], L - 1)
+
+    def step(i):
+        r = i % reps
+        ctx.reserve([seqs[r]], 1, stream)
+        h.graph_launch(graphs[r], stream)
+        ctx.commit([seqs[r]], 1, None, stream)
+        ctx.seq_truncate(seqs[r], L - 1)
+
+    for i in range(args.warmup):
+        step(i)
+    h.stream_sync(stream)
+    e0, e1 = h.event(), h.event()
+    h.record(e0, stream)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    h.record(e1, stream)
+    ms = h.elapsed_ms(e0, e1)
+    wall = time.perf_counter() - t0
+    us_layer = ms * 1e3 / (args.steps * layers)
+    bpl = bytes_per_layer_b(L)
+    gbs = bpl / (us_layer * 1e-6) / 1e9
+
+    # kernel duration: HIP events around individual launches on the same stream
+    n_k = min(args.steps, 250) * layers
+    evs = [(h.event(), h.event()) for _ in range(layers)]
+    tot = 0.0
+    cnt = 0
+    for i in range(n_k // layers):
+        r = i % reps
+        ctx.reserve([seqs[r]], 1, stream)
+        for layer in range(layers):
+            j = r * layers + layer
+            a, b = evs[layer]
+            h.record(a, stream)
+            ctx.decode_attn(layer, [seqs[r]], q.ptr + j * NQ * D * 2, out.ptr + j * NQ * D * 2,
+                            k_new=kn.ptr + j * ROW * 2, v_new=vn.ptr + j * ROW * 2,
+                            out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
+            h.record(b, stream)
+        for layer in range(layers):
+            tot += h.elapsed_ms(*evs[layer])
+            cnt += 1
+        ctx.commit([seqs[r]], 1, None, stream)
+        ctx.seq_truncate(seqs[r], L - 1)
+    kern_us = tot * 1e3 / cnt
+    achieved = bpl / (kern_us * 1e-6) / 1e9
+    for g in graphs:
+        h.graph_destroy(g)
+    for b_ in (q, kn, vn, out):
+        b_.free()
+    ctx.close()
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "b: single-sequence decode step, 8 full-attention layers, 16q/4kv heads, "
+                               "head_dim 256, bf16 cache at 4096 tokens, fused 1-token append + GQA decode "
+                               "per layer, HIP-graph replay, 4 rotated cache replicas (512 MiB)",
+                   "layers": layers, "ctx": L, "replicas": reps},
+        "us_per_layer": round(us_layer, 3),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "bytes_per_layer": bpl,
+        "host_wall_us_per_step": round(wall * 1e6 / args.steps, 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode_kernel", "kernel_avg_us": round(kern_us, 3)},
+    }
+    if not args.no_cpu:
+        res, cores = cpu_baseline_b(L, budget_s=args.cpu_seconds)
+        us1, n1 = res[1]
+        usN, nN = res[cores]
+        line["cpu_baseline"] = {
+            "value": round(bpl / (usN * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+            "us_per_layer": round(usN, 1),
+            "sample": f"oracle decode over 4096 keys, 16 q heads, {nN} layer-decodes on {cores} threads "
+                      f"({cpu_model()})",
+            "single_thread": {"value": round(bpl / (us1 * 1e-6) / 1e9, 2), "unit": "GB/s",
+                              "us_per_layer": round(us1, 1), "layer_decodes": n1},
+        }
+    return line
+
+
+# ---------------------------------------------------------------------------
+# config d: batched paged decode, 64 sequences, ragged contexts
+
+def lengths_d(seed=SEED + 4, n=64, lo=512, hi=32768):
+    rng = np.random.default_rng(seed)
+    return rng.integers(lo, hi + 1, n).astype(np.int64)
+
+
+def bytes_per_layer_d(Ls):
+    # K/V of every key + per seq: q, out (bf16), append read+write; block-table reads
+    Ls = np.asarray(Ls, dtype=np.int64)
+    return int((Ls * ROW * 2 * 2).sum() + len(Ls) * (NQ * D * 2 * 2 + 2 * ROW * 2 * 2)
+               + 4 * ((Ls + BT - 1) // BT).sum())
+
+
+def cpu_baseline_decode(Ls, budget_s):
+    """Oracle batch decode over a bounded sample of sequences (all cores)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import _oracle as O
+
+    cores = host_cores()
+    kcs, vcs = [], []
+    for i, L in enumerate(Ls):
+        kcs.append(O.normal_bf16(int(L) * ROW, SEED + 100 + i))
+        vcs.append(O.normal_bf16(int(L) * ROW, SEED + 200 + i))
+    q = O.normal_bf16(len(Ls) * NQ * D, SEED + 300)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        O.decode_attn_batch(q, kcs, vcs, [int(x) for x in Ls], threads=cores)
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt > budget_s or n >= 50:
+            break
+    return dt / n, cores
+
+
+def run_d(args):
+    import kvc
+
+    h = kvc.hip()
+    layers, nseq = 8, 64
+    Ls = lengths_d()
+    steps, warm = args.d_steps, 2
+    need = int(((Ls + steps + warm + 2 + BT - 1) // BT).sum()) + nseq
+    log(f"config d: {nseq} seqs, L in [{Ls.min()}, {Ls.max()}], sum {Ls.sum()}, pool {need} blocks/layer")
+    ctx = kvc.Context(n_attn_layers=layers, n_ssm_layers=0, max_seqs=nseq, max_seq_len=int(Ls.max()) + 64,
+                      pool_blocks=need, snapshot_slots=0, alloc_seed=SEED + 4)
+    stream = h.stream()
+    ctx.pool_fill_normal(SEED + 4, stream)
+    seqs = [ctx.seq_create() for _ in range(nseq)]
+    for s, L in zip(seqs, Ls):  # ragged synthetic fills, blocks drawn from the permuted pool
+        ctx.reserve([s], int(L), stream)
+        ctx.commit([s], int(L), None, stream)
+    q = h.malloc(layers * nseq * NQ * D * 2)
+    kn = h.malloc(layers * nseq * ROW * 2)
+    vn = h.malloc(layers * nseq * ROW * 2)
+    out = h.malloc(layers * nseq * NQ * D * 2)
+    ctx.fill_normal_bf16(q, layers * nseq * NQ * D, SEED + 40, 1.0, stream)
+    ctx.fill_normal_bf16(kn, layers * nseq * ROW, SEED + 41, 1.0, stream)
+    ctx.fill_normal_bf16(vn, layers * nseq * ROW, SEED + 42, 1.0, stream)
+    h.stream_sync(stream)
+
+    def step():
+        ctx.reserve(seqs, 1, stream)
+        for layer in range(layers):
+            ctx.decode_attn(layer, seqs, q.ptr + layer * nseq * NQ * D * 2, out.ptr + layer * nseq * NQ * D * 2,
+                            k_new=kn.ptr + layer * nseq * ROW * 2, v_new=vn.ptr + layer * nseq * ROW * 2,
+                            out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
+        ctx.commit(seqs, 1, None, stream)
+
+    for _ in range(warm):
+        step()
+    h.stream_sync(stream)
+    L0 = np.array([ctx.seq_len(s) for s in seqs], dtype=np.int64)
+    e0, e1 = h.event(), h.event()
+    h.record(e0, stream)
+    for _ in range(steps):
+        step()
+    h.record(e1, stream)
+    ms = h.elapsed_ms(e0, e1)
+    total_bytes = sum(bytes_per_layer_d(L0 + i + 1) for i in range(steps)) * layers
+    us_layer = ms * 1e3 / (steps * layers)
+    gbs = total_bytes / (ms * 1e-3) / 1e9
+    # one launch timed on its own (kernel duration for the roofline)
+    ctx.reserve(seqs, 1, stream)
+    h.record(e0, stream)
+    ctx.decode_attn(0, seqs, q, out, k_new=kn, v_new=vn, out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
+    h.record(e1, stream)
+    kms = h.elapsed_ms(e0, e1)
+    ctx.commit(seqs, 1, None, stream)
+    L1 = np.array([ctx.seq_len(s) for s in seqs], dtype=np.int64)
+    kbytes = bytes_per_layer_d(L1)
+    for b_ in (q, kn, vn, out):
+        b_.free()
+    ctx.close()
+    res = {"workload": "d: batched paged decode, 64 seqs, ctx U[512,32768] (seeded), block 32, permuted "
+                       "shared pool, 8 layers, fused append + decode per layer",
+           "us_per_layer": round(us_layer, 1), "GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+           "steps": steps, "mean_ctx": float(L0.mean()),
+           "kernel_us": round(kms * 1e3, 1), "kernel_GBps": round(kbytes / (kms * 1e-3) / 1e9, 1),
+           "bytes_per_layer": int(bytes_per_layer_d(L0 + 1))}
+    if not args.no_cpu:
+        rng = np.random.default_rng(SEED + 44)
+        sample = rng.choice(Ls, size=min(8, len(Ls)), replace=False)
+        sec, cores = cpu_baseline_decode(sample, args.cpu_seconds / 2)
+        cb = bytes_per_layer_d(sample)
+        res["cpu_baseline"] = {"value": round(cb / sec / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
+                               "sample": f"oracle decode of {len(sample)} of the 64 sequences (one layer, "
+                                         f"ctx {sorted(int(x) for x in sample)})"}
+    return res
+
+
+# ---------------------------------------------------------------------------
+# config c: multi-turn prefix reuse, 64 sessions, 128-token chunked prefill
+
+def run_c(args):
+    import kvc
+
+    h = kvc.hip()
+    layers, nses, nbase, n_q = 8, 64, 8, 128
+    rng = np.random.default_rng(SEED + 3)
+    bases = rng.integers(0, 151936, (nbase, 3072)).astype(np.int32)
+    P = (rng.integers(256, 3072 + 1, nses) // BT * BT).astype(np.int64)  # reused prefix, block aligned
+    which = rng.integers(0, nbase, nses)
+    need = nbase * (3072 // BT) + int(((n_q + BT - 1) // BT) * nses) + 64
+    ctx = kvc.Context(n_attn_layers=layers, n_ssm_layers=0, max_seqs=nses + nbase, max_seq_len=4096,
+                      pool_blocks=need, snapshot_slots=0, alloc_seed=SEED + 3)
+    stream = h.stream()
+    ctx.pool_fill_normal(SEED + 3, stream)
+    log(f"config c: {nses} sessions, prefix P in [{P.min()}, {P.max()}] mean {P.mean():.0f}")
+    donors = [ctx.seq_create() for _ in range(nbase)]
+    for d_, b_ in zip(donors, bases):  # the earlier turns: prefixes committed with their tokens
+        ctx.reserve([d_], 3072, stream)
+        ctx.commit([d_], 3072, b_, stream)
+    sess = [ctx.seq_create() for _ in range(nses)]
+    t0 = time.perf_counter()
+    reused = []
+    for s, p_, w in zip(sess, P, which):
+        prompt = np.concatenate([bases[w][:p_], rng.integers(0, 151936, n_q).astype(np.int32)])
+        reused.append(ctx.prefix_match(s, prompt, stream))
+    match_us = (time.perf_counter() - t0) * 1e6 / nses
+    reused = np.array(reused)
+    assert (reused == P).all(), "prefix reuse did not return the block-aligned shared prefix"
+    tot_tok = int(reused.sum())
+    kout = h.malloc(tot_tok * ROW * 2)
+    vout = h.malloc(tot_tok * ROW * 2)
+    qb = h.malloc(nses * n_q * NQ * D * 2)
+    kb = h.malloc(nses * n_q * ROW * 2)
+    vb = h.malloc(nses * n_q * ROW * 2)
+    ob = h.malloc(nses * n_q * NQ * D * 2)
+    ctx.fill_normal_bf16(qb, nses * n_q * NQ * D, SEED + 30, 1.0, stream)
+    ctx.fill_normal_bf16(kb, nses * n_q * ROW, SEED + 31, 1.0, stream)
+    ctx.fill_normal_bf16(vb, nses * n_q * ROW, SEED + 32, 1.0, stream)
+    ctx.reserve(sess, n_q, stream)
+    for layer in range(layers):
+        ctx.append(layer, sess, n_q, kb, vb, stream)
+    h.stream_sync(stream)
+    e0, e1, e2 = h.event(), h.event(), h.event()
+    reps = args.c_reps
+    g_ms = p_ms = 0.0
+    for r in range(reps + 1):
+        for layer in range(layers):
+            h.record(e0, stream)
+            ctx.gather(layer, sess, 0, [int(x) for x in reused], kout, vout, stream)
+            h.record(e1, stream)
+            ctx.prefill_attn(layer, sess, n_q, qb, ob, out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
+            h.record(e2, stream)
+            a_ = h.elapsed_ms(e0, e1)
+            b_ = h.elapsed_ms(e1, e2)
+            if r > 0:
+                g_ms += a_
+                p_ms += b_
+    n_meas = reps * layers
+    g_us, p_us = g_ms * 1e3 / n_meas, p_ms * 1e3 / n_meas
+    g_bytes = 2 * 2 * tot_tok * ROW * 2  # K and V, read + write
+    flops = float(sum(16384 * (128 * int(p_) + 8256) for p_ in P))  # causal-exact QK^T + PV
+    p_bytes = int(sum(ROW * 2 * 2 * (int(p_) + n_q) for p_ in P)) + 2 * nses * n_q * NQ * D * 2
+    for b_ in (kout, vout, qb, kb, vb, ob):
+        b_.free()
+    ctx.close()
+    return {"workload": "c: 64 sessions, 8 seeded base streams, block-aligned reused prefix U[256,3072] + 128 "
+                        "unique tokens; gather of the reused blocks + 128-token causal chunked prefill per layer",
+            "prefix_match_us_per_session": round(match_us, 1),
+            "gather_us_per_layer": round(g_us, 1), "gather_GBps": round(g_bytes / (g_us * 1e-6) / 1e9, 1),
+            "prefill_us_per_layer": round(p_us, 1),
+            "prefill_TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 2),
+            "prefill_GBps": round(p_bytes / (p_us * 1e-6) / 1e9, 1),
+            "mean_prefix": float(P.mean())}
+
+
+# ---------------------------------------------------------------------------
+# config e: hybrid prefix-cache snapshot / restore
+
+def run_e(args):
+    import kvc
+
+    h = kvc.hip()
+    nses, iv = 64, 256
+    cfg = dict(n_attn_layers=8, n_ssm_layers=24, max_seqs=2 * nses, max_seq_len=4096, snapshot_slots=nses,
+               snapshot_interval=iv, alloc_seed=SEED + 5)
+    need = 2 * nses * (2 * iv // BT) + 64
+    ctx = kvc.Context(pool_blocks=need, **cfg)
+    stream = h.stream()
+    ctx.pool_fill_normal(SEED + 5, stream)
+    src = [ctx.seq_create() for _ in range(nses)]
+    dst = [ctx.seq_create() for _ in range(nses)]
+    ctx.reserve(src, iv, stream)
+    ctx.commit(src, iv, None, stream)
+    st = ctx.stats()
+    cf = ctx.cfg
+    rec_b = cf.ssm_v_heads * cf.ssm_v_dim * cf.ssm_k_dim * 4
+    conv_b = cf.conv_rows * cf.conv_channels * 4
+    state_bytes = 24 * (rec_b + conv_b)
+    for s in src:  # random live state (fp32 bit patterns from the bf16 generator)
+        r, _ = ctx.state_ptrs(s, 0)
+        ctx.fill_normal_bf16(r, state_bytes // 2, SEED + 50 + s, 1.0, stream)
+    h.stream_sync(stream)
+    e0, e1, e2 = h.event(), h.event(), h.event()
+    reps = args.e_reps
+    sv = rs = 0.0
+    for r in range(reps + 1):
+        h.record(e0, stream)
+        ids = ctx.snapshot_save(src, stream)
+        h.record(e1, stream)
+        ctx.snapshot_restore(dst, ids, stream)
+        h.record(e2, stream)
+        a_, b_ = h.elapsed_ms(e0, e1), h.elapsed_ms(e1, e2)
+        if r > 0:
+            sv += a_
+            rs += b_
+        for i in ids:
+            ctx.snapshot_release(i)
+        for d_ in dst:
+            ctx.seq_reset(d_)
+    per_sess = state_bytes + 8 * 2 * iv * ROW * 2
+    moved = 2 * per_sess * nses  # read + write
+    sv_ms, rs_ms = sv / reps, rs / reps
+    ctx.close()
+    return {"workload": "e: 24 Gated-DeltaNet + 8 attention layers, 64 sessions, save then restore at a 256-token "
+                        "boundary (fp32 recurrent + conv state, bf16 K/V of the segment)",
+            "bytes_per_session": per_sess, "save_ms": round(sv_ms, 3), "restore_ms": round(rs_ms, 3),
+            "save_GBps": round(moved / (sv_ms * 1e-3) / 1e9, 1), "restore_GBps": round(moved / (rs_ms * 1e-3) / 1e9, 1),
+            "hbm_context_bytes": int(st.hbm_bytes)}
+
+
+# ---------------------------------------------------------------------------
+# config a: CPU plumbing (no GPU): prefix match of a 512-token cached prefix
+# on a host-only context, then 1-token append + GQA decode on the oracle
+
+def run_a(args):
+    import kvc
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    import _oracle as O
+
+    rng = np.random.default_rng(SEED + 1)
+    toks = rng.integers(0, 151936, 4096).astype(np.int32)
+    with kvc.Context(device=-1, n_attn_layers=1, n_ssm_layers=0, pool_blocks=512, max_seqs=4,
+                     max_seq_len=8192, snapshot_slots=0) as ctx:
+        a_ = ctx.seq_create()
+        ctx.reserve([a_], 512)
+        ctx.commit([a_], 512, toks[:512])
+        b_ = ctx.seq_create()
+        t0 = time.perf_counter()
+        reuse = ctx.prefix_match(b_, toks)
+        match_us = (time.perf_counter() - t0) * 1e6
+    L = 4096
+    k = O.normal_bf16(L * ROW, SEED + 11)
+    v = O.normal_bf16(L * ROW, SEED + 12)
+    q = O.normal_bf16(NQ * D, SEED + 13)
+    kc = np.zeros(L * ROW, np.uint16)
+    vc = np.zeros(L * ROW, np.uint16)
+    t0 = time.perf_counter()
+    O.L().orc_cache_append(kc.ctypes.data, vc.ctypes.data, NKV, D, 0, L - 1, k.ctypes.data, v.ctypes.data)
+    t1 = time.perf_counter()
+    O.L().orc_cache_append(kc.ctypes.data, vc.ctypes.data, NKV, D, L - 1, 1, k[(L - 1) * ROW:].ctypes.data,
+                           v[(L - 1) * ROW:].ctypes.data)
+    t2 = time.perf_counter()
+    out = O.decode_attn(q, kc, vc, L)
+    t3 = time.perf_counter()
+    return {"workload": "a: CPU plumbing, 1 layer, ctx 4096, 512-token cached prefix match then 1-token append "
+                        "+ GQA decode (16 q heads) on the oracle; no GPU",
+            "prefix_reuse": int(reuse), "prefix_match_us": round(match_us, 1),
+            "append_us": round((t2 - t1) * 1e6, 2), "decode_ms_1thread": round((t3 - t2) * 1e3, 2),
+            "decode_GBps_1thread": round(bytes_per_layer_b(L) / (t3 - t2) / 1e9, 2),
+            "finite": bool(np.isfinite(out).all()), "fill_ms": round((t1 - t0) * 1e3, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", default="all", choices=["all", "a", "b", "c", "d", "e"])
+    ap.add_argument("--d-steps", type=int, default=10)
+    ap.add_argument("--c-reps", type=int, default=2)
+    ap.add_argument("--e-reps", type=int, default=3)
+    ap.add_argument("--replicas", type=int, default=4)
+    ap.add_argument("--chunk-blocks", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the KV path "
+              "shards by sequence or context across GPUs but no multi-GPU run is part of it.",
+              file=sys.stderr)
+        sys.exit(2)
+    runners = {"a": run_a, "c": run_c, "d": run_d, "e": run_e}
+    if args.config in ("all", "b"):
+        line = run_b(args)
+    else:
+        line = {"metric": METRIC, "config": {"workload": args.config}}
+    others = {}
+    for name in ("a", "c", "d", "e"):
+        if args.config in ("all", name):
+            log(f"config {name}")
+            others[name] = runners[name](args)
+    if others:
+        line["configs"] = others
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

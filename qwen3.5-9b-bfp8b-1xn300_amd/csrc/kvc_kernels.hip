@@ -22,17 +22,20 @@ __global__ void table_update_kernel(TableUpdateArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Per-wave online-softmax state.  m/l are wave-uniform; acc[g][j] holds
-// output dims d = lane*4 + j of q head g of the group.
+// Per-wave online-softmax state.  m[g] is wave-uniform (log2 domain); l_lane
+// is this lane's share of the softmax denominator for its own head; acc[g][j]
+// holds output dims d = lane*4 + j of q head g of the group.
 struct WaveState {
     float m[kGroup];
-    float l[kGroup];
+    float l[kGroup];  // filled by finalize_l
+    float l_lane;
     float acc[kGroup][4];
 };
 
-// One block's K/V as held by one wave.
-//   k[i]: token 2i + half of the wave's 8 tokens, dims seg*8 .. seg*8+7 (16 B)
-//   v[j]: token j of the wave's 8 tokens, dims lane*4 .. lane*4+3 (8 B)
+// One block's K/V as held by one wave (the wave owns 8 of the block's 32
+// tokens).  Lane = 16*ts + c (ts = 0..3, c = 0..15):
+//   k[2r + j]: token 4r + ts of the wave's 8, dims (c + 16j)*8 .. +7 (16 B)
+//   v[t]:      token t of the wave's 8, dims lane*4 .. lane*4+3 (8 B)
 struct BlockRegs {
     uint4 k[4];
     uint2 v[kTokPerWave];
@@ -46,144 +49,203 @@ __device__ __forceinline__ void init_state(WaveState& st) {
 #pragma unroll
         for (int j = 0; j < 4; j++) st.acc[g][j] = 0.f;
     }
+    st.l_lane = 0.f;
 }
 
-// Load the wave's share of one (block, kv_head) unit.  Tokens >= n_valid read
-// as zero.  The token at slot new_slot (if >= 0) comes from knew/vnew (one
-// token row of this kv head) and is also written into the pool unit.
+// Load the wave's share of one (block, kv_head) unit with unconditional
+// 16-B / 8-B loads (every slot of an allocated unit is addressable; slots past
+// the sequence end are masked in compute_block).
 __device__ __forceinline__ void load_block(BlockRegs& r, const uint16_t* __restrict__ ku,
-                                           const uint16_t* __restrict__ vu, int n_valid,
-                                           int new_slot, const uint16_t* knew,
-                                           const uint16_t* vnew, int wave, int lane) {
-    const int half = lane >> 5, seg = lane & 31;
+                                           const uint16_t* __restrict__ vu, int wave, int lane) {
+    const int ts = lane >> 4, c = lane & 15;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int t = wave * kTokPerWave + 2 * i + half;
-        uint4 x = make_uint4(0, 0, 0, 0);
-        if (t == new_slot) {
-            x = *reinterpret_cast<const uint4*>(knew + seg * 8);
-            *reinterpret_cast<uint4*>(const_cast<uint16_t*>(ku) + t * kHeadDim + seg * 8) = x;
-        } else if (t < n_valid) {
-            { const u32x4 y = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ku + t * kHeadDim + seg * 8)); x = make_uint4(y[0], y[1], y[2], y[3]); }
+    for (int rr = 0; rr < 2; rr++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int t = wave * kTokPerWave + rr * 4 + ts;
+            const u32x4 y = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(ku + t * kHeadDim + (c + 16 * j) * 8));
+            r.k[rr * 2 + j] = make_uint4(y[0], y[1], y[2], y[3]);
         }
-        r.k[i] = x;
     }
 #pragma unroll
-    for (int j = 0; j < kTokPerWave; j++) {
-        const int t = wave * kTokPerWave + j;
-        uint2 x = make_uint2(0, 0);
-        if (t == new_slot) {
-            x = *reinterpret_cast<const uint2*>(vnew + lane * 4);
-            *reinterpret_cast<uint2*>(const_cast<uint16_t*>(vu) + t * kHeadDim + lane * 4) = x;
-        } else if (t < n_valid) {
-            { const u32x2 y = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(vu + t * kHeadDim + lane * 4)); x = make_uint2(y[0], y[1]); }
-        }
-        r.v[j] = x;
+    for (int t = 0; t < kTokPerWave; t++) {
+        const u32x2 y = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x2*>(vu + (wave * kTokPerWave + t) * kHeadDim + lane * 4));
+        r.v[t] = make_uint2(y[0], y[1]);
     }
 }
+
+// DPP lane moves inside rows of 16 (no LDS traffic).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRowRor8 = 0x128;    // lane ^ 8 inside a row of 16
+constexpr int kDppRowMirror = 0x140;  // lane -> 15 - lane inside a row
+constexpr int kDppHalfMirror = 0x141; // lane -> 7 - lane inside 8 lanes
+
+// x(lane) op x(lane ^ 16) / x(lane ^ 32) through v_permlane*_swap.
+__device__ __forceinline__ float sum_xor16(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float x) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(f32_to_bf16_rne(x) << 16); }
 
 // Scores, online softmax update and P.V for one block held in registers.
-// qv[g][c]: packed bf16 pairs of q head g, dims seg*8 + 2c, +1.
-__device__ __forceinline__ void compute_block(const BlockRegs& r, const uint32_t (&qv)[kGroup][4],
-                                              int n_valid, float scale_log2, float* lds_p,
+// qv[g][j][i]: packed bf16 pairs of q head g, dims (c + 16j)*8 + 2i, +1.
+// lds_p16: per-wave 32 bf16 p values laid out [g][token].
+__device__ __forceinline__ void compute_block(BlockRegs& r, const uint32_t (&qv)[kGroup][2][4],
+                                              int n_valid, float scale_log2, uint16_t* lds_p16,
                                               WaveState& st, int wave, int lane) {
-    const int half = lane >> 5, seg = lane & 31;
-    // partial q.k over this lane's 8 dims for 4 tokens x 4 heads
-    float a[16];
+    const int ts = lane >> 4, c = lane & 15;
+    // partial q.k over this lane's 16 dims: a[4*rr + g] for tokens 4rr + ts
+    float a[8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int rr = 0; rr < 2; rr++) {
 #pragma unroll
         for (int g = 0; g < kGroup; g++) {
-            float s = dot2_bf16(qv[g][0], r.k[i].x, 0.f);
-            s = dot2_bf16(qv[g][1], r.k[i].y, s);
-            s = dot2_bf16(qv[g][2], r.k[i].z, s);
-            s = dot2_bf16(qv[g][3], r.k[i].w, s);
-            a[i * 4 + g] = s;
+            float x = 0.f;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint4 k = r.k[rr * 2 + j];
+                x = dot2_bf16(qv[g][j][0], k.x, x);
+                x = dot2_bf16(qv[g][j][1], k.y, x);
+                x = dot2_bf16(qv[g][j][2], k.z, x);
+                x = dot2_bf16(qv[g][j][3], k.w, x);
+            }
+            a[rr * 4 + g] = x;
         }
     }
-    // transpose-reduce over the 32 lanes of a half: after the steps over seg
-    // bits 4..1, a[0] holds value index (seg >> 1) summed over 16 lanes.
-#define KVC_TR_STEP(BIT, N)                                                  \
-    {                                                                        \
-        const bool sel = (seg >> BIT) & 1;                                   \
-        _Pragma("unroll") for (int j = 0; j < N / 2; j++) {                  \
-            float send = sel ? a[j] : a[j + N / 2];                          \
-            float keep = sel ? a[j + N / 2] : a[j];                          \
-            a[j] = keep + shfl_xor<(1 << BIT)>(send);                        \
-        }                                                                    \
+    // transpose-reduce over the 16 lanes of a token (c bits 3, 2, 1, then 0).
+    // Each step pairs lanes that differ in the step's bit and agree on the
+    // bits already decided; the mirror moves also flip lower, still
+    // undecided bits, which is harmless.
+#define KVC_TR(BIT, N, CTRL)                                             \
+    {                                                                    \
+        const bool sel = (c >> BIT) & 1;                                 \
+        _Pragma("unroll") for (int j = 0; j < N / 2; j++) {              \
+            const float send = sel ? a[j] : a[j + N / 2];                \
+            const float keep = sel ? a[j + N / 2] : a[j];                \
+            a[j] = keep + dpp<CTRL>(send);                               \
+        }                                                                \
     }
-    KVC_TR_STEP(4, 16)
-    KVC_TR_STEP(3, 8)
-    KVC_TR_STEP(2, 4)
-    KVC_TR_STEP(1, 2)
-#undef KVC_TR_STEP
-    float sc = a[0] + shfl_xor<1>(a[0]);
-    const int vi = seg >> 1;
+    KVC_TR(3, 8, kDppRowMirror)
+    KVC_TR(2, 4, kDppHalfMirror)
+    KVC_TR(1, 2, kDppXor2)
+#undef KVC_TR
+    float sc = a[0] + dpp<kDppXor1>(a[0]);
+    const int vi = (c >> 1) & 7;
     const int my_g = vi & 3;
-    const int t_loc = 2 * (vi >> 2) + half;  // token within the wave's 8
+    const int t_loc = (vi >> 2) * 4 + ts;  // token within the wave's 8
     const bool valid = wave * kTokPerWave + t_loc < n_valid;
     sc = valid ? sc * scale_log2 : kNegBig;
 
-    // block max per head over the wave's 8 tokens
-    float mx = sc;
-    mx = fmaxf(mx, shfl_xor<8>(mx));
-    mx = fmaxf(mx, shfl_xor<16>(mx));
-    mx = fmaxf(mx, shfl_xor<32>(mx));
-    float mref_own = 0.f;
+    // lazy running max: rescale only when a score passes its head's max by
+    // more than the slack (p stays <= 2^slack)
+    float m_own = st.m[0];
 #pragma unroll
-    for (int g = 0; g < kGroup; g++) {
-        const float mb = readlane(mx, g << 1);
-        if (mb > st.m[g] + kRescaleSlack) {
-            const float c = fast_exp2(st.m[g] - mb);
-            st.l[g] *= c;
-#pragma unroll
-            for (int j = 0; j < 4; j++) st.acc[g][j] *= c;
-            st.m[g] = mb;
-        }
-        mref_own = (my_g == g) ? st.m[g] : mref_own;
-    }
-    const float p = valid ? fast_exp2(sc - mref_own) : 0.f;
-    float ps = p;
-    ps += shfl_xor<8>(ps);
-    ps += shfl_xor<16>(ps);
-    ps += shfl_xor<32>(ps);
-#pragma unroll
-    for (int g = 0; g < kGroup; g++) st.l[g] += readlane(ps, g << 1);
-
-    // broadcast p[token][g] through LDS (per-wave area of 32 floats)
-    wave_lds_sync();
-    if ((seg & 1) == 0) lds_p[t_loc * 4 + my_g] = p;
-    wave_lds_sync();
-#pragma unroll
-    for (int j = 0; j < kTokPerWave; j++) {
-        const float4 pj = *reinterpret_cast<const float4*>(lds_p + j * 4);
-        const float v0 = bf16lo(r.v[j].x), v1 = bf16hi(r.v[j].x);
-        const float v2 = bf16lo(r.v[j].y), v3 = bf16hi(r.v[j].y);
-        const float pg[4] = {pj.x, pj.y, pj.z, pj.w};
+    for (int g = 1; g < kGroup; g++) m_own = (my_g == g) ? st.m[g] : m_own;
+    if (__builtin_amdgcn_ballot_w64(sc > m_own + kRescaleSlack) != 0) {
+        float mx = sc;
+        mx = fmaxf(mx, dpp<kDppRowRor8>(mx));
+        mx = max_xor16(mx);
+        mx = max_xor32(mx);
+        float c_own = 1.f;
 #pragma unroll
         for (int g = 0; g < kGroup; g++) {
-            st.acc[g][0] = fmaf(pg[g], v0, st.acc[g][0]);
-            st.acc[g][1] = fmaf(pg[g], v1, st.acc[g][1]);
-            st.acc[g][2] = fmaf(pg[g], v2, st.acc[g][2]);
-            st.acc[g][3] = fmaf(pg[g], v3, st.acc[g][3]);
+            const float mb = readlane(mx, g << 1);
+            if (mb > st.m[g] + kRescaleSlack) {
+                const float cg = fast_exp2(st.m[g] - mb);
+#pragma unroll
+                for (int j = 0; j < 4; j++) st.acc[g][j] *= cg;
+                c_own = (my_g == g) ? cg : c_own;
+                st.m[g] = mb;
+            }
+        }
+        st.l_lane *= c_own;
+        m_own = st.m[0];
+#pragma unroll
+        for (int g = 1; g < kGroup; g++) m_own = (my_g == g) ? st.m[g] : m_own;
+    }
+    // p rounded to bf16 once; the same value feeds l and P.V
+    const float p = valid ? bf16_round(fast_exp2(sc - m_own)) : 0.f;
+    st.l_lane += p;
+
+    // broadcast p as bf16 [g][token] through LDS
+    wave_lds_sync();
+    if ((c & 1) == 0) lds_p16[my_g * kTokPerWave + t_loc] = (uint16_t)(__float_as_uint(p) >> 16);
+    wave_lds_sync();
+    uint4 pp[kGroup];  // pp[g].{x,y,z,w} = (p[g][2k], p[g][2k+1]) for k = 0..3
+#pragma unroll
+    for (int g = 0; g < kGroup; g++) pp[g] = *reinterpret_cast<const uint4*>(lds_p16 + g * kTokPerWave);
+
+    if (n_valid < (wave + 1) * kTokPerWave) {  // partial block: stale slots may hold NaN bits
+#pragma unroll
+        for (int t = 0; t < kTokPerWave; t++)
+            if (wave * kTokPerWave + t >= n_valid) r.v[t] = make_uint2(0, 0);
+    }
+    // P.V on token pairs with v_dot2_f32_bf16: (v[2k][d], v[2k+1][d]) packed
+#pragma unroll
+    for (int k = 0; k < kTokPerWave / 2; k++) {
+        const uint2 v0 = r.v[2 * k], v1 = r.v[2 * k + 1];
+        uint32_t vp[4];
+        vp[0] = __builtin_amdgcn_perm(v1.x, v0.x, 0x05040100u);
+        vp[1] = __builtin_amdgcn_perm(v1.x, v0.x, 0x07060302u);
+        vp[2] = __builtin_amdgcn_perm(v1.y, v0.y, 0x05040100u);
+        vp[3] = __builtin_amdgcn_perm(v1.y, v0.y, 0x07060302u);
+#pragma unroll
+        for (int g = 0; g < kGroup; g++) {
+            const uint32_t pk = k == 0 ? pp[g].x : k == 1 ? pp[g].y : k == 2 ? pp[g].z : pp[g].w;
+#pragma unroll
+            for (int j = 0; j < 4; j++) st.acc[g][j] = dot2_bf16(pk, vp[j], st.acc[g][j]);
         }
     }
 }
 
-__device__ __forceinline__ void load_q(uint32_t (&qv)[kGroup][4], const uint16_t* qhead0, int seg) {
+// Reduce the per-lane denominators to st.l[g] (wave-uniform).
+__device__ __forceinline__ void finalize_l(WaveState& st) {
+    float x = st.l_lane;
+    x += dpp<kDppRowRor8>(x);
+    x = sum_xor16(x);
+    x = sum_xor32(x);
+#pragma unroll
+    for (int g = 0; g < kGroup; g++) st.l[g] = readlane(x, g << 1);
+}
+
+__device__ __forceinline__ void load_q(uint32_t (&qv)[kGroup][2][4], const uint16_t* qhead0, int lane) {
+    const int c = lane & 15;
 #pragma unroll
     for (int g = 0; g < kGroup; g++) {
-        const uint4 x = *reinterpret_cast<const uint4*>(qhead0 + g * kHeadDim + seg * 8);
-        qv[g][0] = x.x;
-        qv[g][1] = x.y;
-        qv[g][2] = x.z;
-        qv[g][3] = x.w;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint4 x = *reinterpret_cast<const uint4*>(qhead0 + g * kHeadDim + (c + 16 * j) * 8);
+            qv[g][j][0] = x.x;
+            qv[g][j][1] = x.y;
+            qv[g][j][2] = x.z;
+            qv[g][j][3] = x.w;
+        }
     }
 }
 
 // LDS for one workgroup: per-wave p broadcast + cross-wave merge area.
 struct DecodeSmem {
-    float p[kWaves][32];
+    uint16_t p16[kWaves][32];
     float acc[kWaves][kGroup][kHeadDim];
     float ml[kWaves][kGroup][2];
     int last;
@@ -249,12 +311,118 @@ __device__ __forceinline__ void write_out(void* out, int out_bf16, size_t row_of
     }
 }
 
+// Fused append: copy the new token's K and V rows of kv head h (512 B each)
+// into its pool slot.  Run by the one workgroup whose chunk holds the slot,
+// after its block walk (which never reads that slot), so no store sits inside
+// the load pipeline.
+__device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpool, const int32_t* trow,
+                                                 int h, int pos, const uint16_t* knew,
+                                                 const uint16_t* vnew) {
+    const int t = threadIdx.x;
+    if (t >= 64) return;
+    const size_t off = (((size_t)trow[pos / kBlockTok] * kKvHeads + h) * kBlockTok + pos % kBlockTok) * kHeadDim;
+    const int kv = t >> 5, part = t & 31;
+    const uint16_t* src = (kv ? vnew : knew) + part * 8;
+    uint16_t* dst = (kv ? vpool : kpool) + off + part * 8;
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+}
+
+// ---------------------------------------------------------------------------
+// Walk blocks [blk0, blk1) of one (sequence, kv head) with two register
+// buffers (the next block's loads are in flight while the current one is
+// computed).  Block ids are fetched once per 64 blocks into a VGPR and read
+// back per block with v_readlane, so no table load sits on the critical path.
+// Walk blocks [blk0, blk1) of one (sequence, kv head); keys at positions >= L
+// are masked.  Block ids are fetched once per 64 blocks into a VGPR and read
+// back per block with v_readlane, so no table load sits in the pipeline.
+// Each iteration is straight-line code over 4 blocks and 2 register buffers:
+// loads are unconditional (indices past the window are clamped to its last
+// block and their compute is skipped), so the wait before each compute covers
+// exactly the buffer it reads while the other buffer stays in flight.
+__device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
+                                            const uint16_t* __restrict__ vpool,
+                                            const int32_t* __restrict__ trow, int h, int blk0,
+                                            int blk1, int L, const uint32_t (&qv)[kGroup][2][4],
+                                            float scale_log2, uint16_t* lds_p, WaveState& st,
+                                            int wave, int lane) {
+    BlockRegs r0, r1;
+    constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
+#define KVC_LOAD_WIN(R, I)                                                                          \
+    {                                                                                               \
+        const int ii_ = min((I), wn - 1);                                                           \
+        const size_t off_ = ((size_t)__builtin_amdgcn_readlane(my_id, ii_) * kKvHeads + h) * kUnitElems; \
+        load_block(R, kpool + off_, vpool + off_, wave, lane);                                     \
+    }
+    for (int w0 = blk0; w0 < blk1; w0 += 64) {
+        const int wn = min(64, blk1 - w0);
+        const int my_id = lane < wn ? trow[w0 + lane] : 0;
+        for (int i = 0; i < wn; i += 4) {
+            const int nv0 = min(kBlockTok, L - (w0 + i) * kBlockTok);
+            const int nv1 = min(kBlockTok, L - (w0 + i + 1) * kBlockTok);
+            const int nv2 = min(kBlockTok, L - (w0 + i + 2) * kBlockTok);
+            const int nv3 = min(kBlockTok, L - (w0 + i + 3) * kBlockTok);
+            KVC_LOAD_WIN(r0, i)
+            KVC_LOAD_WIN(r1, i + 1)
+            compute_block(r0, qv, nv0, scale_log2, lds_p, st, wave, lane);
+            KVC_LOAD_WIN(r0, i + 2)
+            if (i + 1 < wn) compute_block(r1, qv, nv1, scale_log2, lds_p, st, wave, lane);
+            KVC_LOAD_WIN(r1, i + 3)
+            if (i + 2 < wn) compute_block(r0, qv, nv2, scale_log2, lds_p, st, wave, lane);
+            if (i + 3 < wn) compute_block(r1, qv, nv3, scale_log2, lds_p, st, wave, lane);
+        }
+    }
+#undef KVC_LOAD_WIN
+}
+
+// Fold one extra key (the fused-append token, bf16 rows knew/vnew of this kv
+// head) into a wave's finalized state (uniform m, l).  Each group of 16 lanes
+// holds all 256 dims of q.
+__device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[kGroup][2][4],
+                                           const uint16_t* knew, const uint16_t* vnew,
+                                           float scale_log2, int lane) {
+    const int c = lane & 15;
+    const uint4 k0 = *reinterpret_cast<const uint4*>(knew + c * 8);
+    const uint4 k1 = *reinterpret_cast<const uint4*>(knew + (c + 16) * 8);
+    float sc[kGroup];
+#pragma unroll
+    for (int g = 0; g < kGroup; g++) {
+        float x = dot2_bf16(qv[g][0][0], k0.x, 0.f);
+        x = dot2_bf16(qv[g][0][1], k0.y, x);
+        x = dot2_bf16(qv[g][0][2], k0.z, x);
+        x = dot2_bf16(qv[g][0][3], k0.w, x);
+        x = dot2_bf16(qv[g][1][0], k1.x, x);
+        x = dot2_bf16(qv[g][1][1], k1.y, x);
+        x = dot2_bf16(qv[g][1][2], k1.z, x);
+        x = dot2_bf16(qv[g][1][3], k1.w, x);
+        x += dpp<kDppXor1>(x);
+        x += dpp<kDppXor2>(x);
+        x += dpp<kDppHalfMirror>(x);  // after xor 1, 2 every lane of a quad agrees
+        x += dpp<kDppRowRor8>(x);
+        sc[g] = readlane(x, 0) * scale_log2;
+    }
+    const uint2 v = *reinterpret_cast<const uint2*>(vnew + lane * 4);
+    const float vf[4] = {bf16lo(v.x), bf16hi(v.x), bf16lo(v.y), bf16hi(v.y)};
+#pragma unroll
+    for (int g = 0; g < kGroup; g++) {
+        const float mn = fmaxf(st.m[g], sc[g]);
+        const float cg = fast_exp2(st.m[g] - mn);
+        const float p = fast_exp2(sc[g] - mn);
+        st.l[g] = fmaf(st.l[g], cg, p);
+#pragma unroll
+        for (int j = 0; j < 4; j++) st.acc[g][j] = fmaf(st.acc[g][j], cg, p * vf[j]);
+        st.m[g] = mn;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Split-K GQA decode.  Work item = (kv head, chunk of chunk_blocks blocks of
 // one sequence); items of one (seq, head) are consecutive and are spread over
 // the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8).  Each item
 // writes (m, l, acc) for its 4 q heads; the last item of a (seq, head) to
 // arrive (device-scope counter) combines them and writes the output.
+constexpr int kItemFloats = kGroup * kHeadDim + 2 * kGroup;
+constexpr int kCombineBatch = 16;
+
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     __shared__ DecodeSmem sm;
     const int b = blockIdx.x;
@@ -270,40 +438,29 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     const int n_blocks = (L + kBlockTok - 1) / kBlockTok;
     const int blk0 = c * a.chunk_blocks;
     const int blk1 = min(blk0 + a.chunk_blocks, n_blocks);
-    const int slot = a.slot[s];
-    const int* trow = a.table + (size_t)slot * a.table_stride;
+    const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, seg = lane & 31;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int new_pos = a.k_new ? L - 1 : -1;
     const uint16_t* knew = a.k_new ? a.k_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
     const uint16_t* vnew = a.v_new ? a.v_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
 
-    uint32_t qv[kGroup][4];
-    load_q(qv, a.q + ((size_t)s * kQHeads + h * kGroup) * kHeadDim, seg);
-
+    uint32_t qv[kGroup][2][4];
+    load_q(qv, a.q + ((size_t)s * kQHeads + h * kGroup) * kHeadDim, lane);
     WaveState st;
     init_state(st);
-    BlockRegs r0, r1;
-    auto unit = [&](const uint16_t* pool, int blk) {
-        return pool + ((size_t)trow[blk] * kKvHeads + h) * (kBlockTok * kHeadDim);
-    };
-    auto nvalid = [&](int blk) { return min(kBlockTok, L - blk * kBlockTok); };
-    auto nslot = [&](int blk) {
-        const int d = new_pos - blk * kBlockTok;
-        return (d >= 0 && d < kBlockTok) ? d : -1;
-    };
-    load_block(r0, unit(a.kpool, blk0), unit(a.vpool, blk0), nvalid(blk0), nslot(blk0), knew, vnew,
-               wave, lane);
-    for (int blk = blk0; blk < blk1; blk += 2) {
-        if (blk + 1 < blk1)
-            load_block(r1, unit(a.kpool, blk + 1), unit(a.vpool, blk + 1), nvalid(blk + 1),
-                       nslot(blk + 1), knew, vnew, wave, lane);
-        compute_block(r0, qv, nvalid(blk), a.scale_log2, sm.p[wave], st, wave, lane);
-        if (blk + 1 >= blk1) break;
-        if (blk + 2 < blk1)
-            load_block(r0, unit(a.kpool, blk + 2), unit(a.vpool, blk + 2), nvalid(blk + 2),
-                       nslot(blk + 2), knew, vnew, wave, lane);
-        compute_block(r1, qv, nvalid(blk + 1), a.scale_log2, sm.p[wave], st, wave, lane);
+    // keys [0, Lw) come from the pool; with a fused append the last key
+    // (position L-1) comes from knew/vnew and is folded in by wave 0 of the
+    // chunk that owns it, which also writes it into the pool
+    const int Lw = a.k_new ? L - 1 : L;
+    const int wblk1 = min(blk1, (Lw + kBlockTok - 1) / kBlockTok);
+    walk_blocks(a.kpool, a.vpool, trow, h, blk0, wblk1, Lw, qv, a.scale_log2, sm.p16[wave], st, wave, lane);
+    finalize_l(st);
+    const bool owns_new = new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
+    if (owns_new) {
+        if (wave == 0) fold_token(st, qv, knew, vnew, a.scale_log2, lane);
+        append_new_token(const_cast<uint16_t*>(a.kpool), const_cast<uint16_t*>(a.vpool), trow, h, new_pos,
+                         knew, vnew);
     }
 
     float M, Lsum, A[4];
@@ -315,13 +472,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
         write_out(a.out, a.out_bf16, orow, d0, grow, Lsum, A);
         return;
     }
-    constexpr int kItemFloats = kGroup * kHeadDim + 2 * kGroup;
     float* part = a.part + (size_t)item * kItemFloats;
     *reinterpret_cast<float4*>(part + g * kHeadDim + d0) = make_float4(A[0], A[1], A[2], A[3]);
-    if ((t & 63) == 0) {
-        part[kGroup * kHeadDim + 2 * g] = M;
-        part[kGroup * kHeadDim + 2 * g + 1] = Lsum;
-    }
+    if ((t & 63) == 0) *reinterpret_cast<float2*>(part + kGroup * kHeadDim + 2 * g) = make_float2(M, Lsum);
     __threadfence();
     __syncthreads();
     if (t == 0) {
@@ -331,26 +484,37 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     __syncthreads();
     if (!sm.last) return;
     __threadfence();
-    // combine the n_chunks partials of (s, h)
-    const size_t first = (size_t)h * a.total_chunks + a.chunk_begin[s];
+    // combine the n_chunks partials of (s, h); loads of a batch are all issued
+    // before any is used
+    const float* first = a.part + ((size_t)h * a.total_chunks + a.chunk_begin[s]) * kItemFloats;
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < n_chunks; k++) {
-        const float* pk = a.part + (first + k) * kItemFloats;
-        const float mk = pk[kGroup * kHeadDim + 2 * g];
-        const float lk = pk[kGroup * kHeadDim + 2 * g + 1];
-        const f32x4 ak = *reinterpret_cast<const f32x4*>(pk + g * kHeadDim + d0);
-        if (mk > Mc) {
-            const float cc = fast_exp2(Mc - mk);
-            Lc *= cc;
-            Ac[0] *= cc; Ac[1] *= cc; Ac[2] *= cc; Ac[3] *= cc;
-            Mc = mk;
+    for (int k0 = 0; k0 < n_chunks; k0 += kCombineBatch) {
+        f32x4 av[kCombineBatch];
+        float2 ml[kCombineBatch];
+#pragma unroll
+        for (int k = 0; k < kCombineBatch; k++) {
+            const int kk = min(k0 + k, n_chunks - 1);
+            const float* pk = first + (size_t)kk * kItemFloats;
+            av[k] = *reinterpret_cast<const f32x4*>(pk + g * kHeadDim + d0);
+            ml[k] = *reinterpret_cast<const float2*>(pk + kGroup * kHeadDim + 2 * g);
         }
-        const float w = fast_exp2(mk - Mc);
-        Lc = fmaf(w, lk, Lc);
-        Ac[0] = fmaf(w, ak[0], Ac[0]);
-        Ac[1] = fmaf(w, ak[1], Ac[1]);
-        Ac[2] = fmaf(w, ak[2], Ac[2]);
-        Ac[3] = fmaf(w, ak[3], Ac[3]);
+        float mb = Mc;
+#pragma unroll
+        for (int k = 0; k < kCombineBatch; k++)
+            if (k0 + k < n_chunks) mb = fmaxf(mb, ml[k].x);
+        const float cc = fast_exp2(Mc - mb);
+        Lc *= cc;
+        Ac[0] *= cc; Ac[1] *= cc; Ac[2] *= cc; Ac[3] *= cc;
+        Mc = mb;
+#pragma unroll
+        for (int k = 0; k < kCombineBatch; k++) {
+            const float w = (k0 + k < n_chunks) ? fast_exp2(ml[k].x - Mc) : 0.f;
+            Lc = fmaf(w, ml[k].y, Lc);
+            Ac[0] = fmaf(w, av[k][0], Ac[0]);
+            Ac[1] = fmaf(w, av[k][1], Ac[1]);
+            Ac[2] = fmaf(w, av[k][2], Ac[2]);
+            Ac[3] = fmaf(w, av[k][3], Ac[3]);
+        }
     }
     write_out(a.out, a.out_bf16, orow, d0, grow, Lc, Ac);
     if (t == 0) a.counters[s * kKvHeads + h] = 0;
@@ -366,21 +530,16 @@ __global__ __launch_bounds__(kThreads) void prefill_rowwise_kernel(PrefillArgs a
     const int s = blockIdx.x / (kKvHeads * a.n_q);
     const int L = a.q_pos0[s] + row + 1;
     const int n_blocks = (L + kBlockTok - 1) / kBlockTok;
-    const int* trow = a.table + (size_t)a.slot[s] * a.table_stride;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, seg = lane & 31;
+    const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t qrow = (((size_t)s * a.n_q + row) * kQHeads + h * kGroup) * kHeadDim;
 
-    uint32_t qv[kGroup][4];
-    load_q(qv, a.q + qrow, seg);
+    uint32_t qv[kGroup][2][4];
+    load_q(qv, a.q + qrow, lane);
     WaveState st;
     init_state(st);
-    BlockRegs r0;
-    for (int blk = 0; blk < n_blocks; blk++) {
-        const size_t uoff = ((size_t)trow[blk] * kKvHeads + h) * (kBlockTok * kHeadDim);
-        const int nv = min(kBlockTok, L - blk * kBlockTok);
-        load_block(r0, a.kpool + uoff, a.vpool + uoff, nv, -1, nullptr, nullptr, wave, lane);
-        compute_block(r0, qv, nv, a.scale_log2, sm.p[wave], st, wave, lane);
-    }
+    walk_blocks(a.kpool, a.vpool, trow, h, 0, n_blocks, L, qv, a.scale_log2, sm.p16[wave], st, wave, lane);
+    finalize_l(st);
     float M, Lsum, A[4];
     merge_waves(st, sm, wave, lane, M, Lsum, A);
     const int t = threadIdx.x, g = t >> 6, d0 = (t & 63) * 4;

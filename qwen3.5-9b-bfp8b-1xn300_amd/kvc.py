@@ -175,6 +175,12 @@ class Hip:
         L.hipGetErrorString.restype = ctypes.c_char_p
         L.hipGetErrorString.argtypes = [ctypes.c_int]
         L.hipMemGetInfo.argtypes = [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
+        L.hipStreamBeginCapture.argtypes = [P, ctypes.c_int]
+        L.hipStreamEndCapture.argtypes = [P, ctypes.POINTER(P)]
+        L.hipGraphInstantiate.argtypes = [ctypes.POINTER(P), P, P, P, ctypes.c_size_t]
+        L.hipGraphLaunch.argtypes = [P, P]
+        L.hipGraphExecDestroy.argtypes = [P]
+        L.hipGraphDestroy.argtypes = [P]
 
     def ok(self, rc, what):
         if rc != 0:
@@ -211,6 +217,26 @@ class Hip:
         ms = ctypes.c_float()
         self.ok(self.L.hipEventElapsedTime(ctypes.byref(ms), e0, e1), "hipEventElapsedTime")
         return ms.value
+
+    def capture(self, stream, fn):
+        """Capture the work fn() enqueues on `stream` into an executable graph."""
+        self.ok(self.L.hipStreamBeginCapture(stream, 0), "hipStreamBeginCapture")
+        try:
+            fn()
+        finally:
+            g = ctypes.c_void_p()
+            rc = self.L.hipStreamEndCapture(stream, ctypes.byref(g))
+        self.ok(rc, "hipStreamEndCapture")
+        ex = ctypes.c_void_p()
+        self.ok(self.L.hipGraphInstantiate(ctypes.byref(ex), g, None, None, 0), "hipGraphInstantiate")
+        self.L.hipGraphDestroy(g)
+        return ex.value
+
+    def graph_launch(self, ex, stream):
+        self.ok(self.L.hipGraphLaunch(ex, stream), "hipGraphLaunch")
+
+    def graph_destroy(self, ex):
+        self.L.hipGraphExecDestroy(ex)
 
     def stream_sync(self, stream):
         self.ok(self.L.hipStreamSynchronize(stream), "hipStreamSynchronize")
