@@ -60,4 +60,13 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer access with cache-policy bits.  kCpolSC1 marks an access as
+// coherent at agent (device) scope: stores write through the XCD's L2 and
+// loads do not take a stale line from it, so data can pass between
+// workgroups on different XCDs without a full L2 writeback (buffer_wbl2).
+constexpr int kCpolSC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
 }  // namespace kvc

@@ -33,6 +33,10 @@ constexpr size_t kBlockBytes = kUnitBytes * kKvHeads;            // 64 KiB
 
 constexpr int kMaxBatch = 64;        // seqs per kernel launch (argument block)
 constexpr int kMaxChunks = 8192;     // split-K work chunks per decode launch
+// split-K partial of one work item: acc [4 q heads][256] fp32 then (m, l) per
+// head, padded to whole 128-B lines so no line is shared by two items
+constexpr int kItemFloats = 1056;
+constexpr size_t kPartBytes = (size_t)kMaxChunks * kKvHeads * kItemFloats * 4;
 constexpr int kTableUpdatesPerLaunch = 480;
 
 // ---- kernel argument blocks (passed by value; must stay < 4 KiB) ----------

@@ -420,7 +420,6 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
 // the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8).  Each item
 // writes (m, l, acc) for its 4 q heads; the last item of a (seq, head) to
 // arrive (device-scope counter) combines them and writes the output.
-constexpr int kItemFloats = kGroup * kHeadDim + 2 * kGroup;
 constexpr int kCombineBatch = 16;
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
@@ -472,48 +471,62 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
         write_out(a.out, a.out_bf16, orow, d0, grow, Lsum, A);
         return;
     }
-    float* part = a.part + (size_t)item * kItemFloats;
-    *reinterpret_cast<float4*>(part + g * kHeadDim + d0) = make_float4(A[0], A[1], A[2], A[3]);
-    if ((t & 63) == 0) *reinterpret_cast<float2*>(part + kGroup * kHeadDim + 2 * g) = make_float2(M, Lsum);
-    __threadfence();
+    // publish (m, l, acc) with agent-coherent 16-B stores; once they have all
+    // completed (s_waitcnt 0) the arrival counter is bumped.  The last item of
+    // (s, h) to arrive reads the partials back with agent-coherent loads.
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.part, (uint32_t)kPartBytes);
+    const int ibase = item * kItemFloats * 4;
+    u32x4 av;
+    av[0] = __float_as_uint(A[0]);
+    av[1] = __float_as_uint(A[1]);
+    av[2] = __float_as_uint(A[2]);
+    av[3] = __float_as_uint(A[3]);
+    __builtin_amdgcn_raw_buffer_store_b128(av, prs, ibase + (g * kHeadDim + d0) * 4, 0, kCpolSC1);
+    if ((t & 63) == 0) {
+        u32x2 mlv;
+        mlv[0] = __float_as_uint(M);
+        mlv[1] = __float_as_uint(Lsum);
+        __builtin_amdgcn_raw_buffer_store_b64(mlv, prs, ibase + (kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (t == 0) {
-        const int prev = atomicAdd(&a.counters[s * kKvHeads + h], 1);
+        const int prev = __hip_atomic_fetch_add(&a.counters[s * kKvHeads + h], 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
         sm.last = (prev == n_chunks - 1);
     }
     __syncthreads();
     if (!sm.last) return;
-    __threadfence();
     // combine the n_chunks partials of (s, h); loads of a batch are all issued
     // before any is used
-    const float* first = a.part + ((size_t)h * a.total_chunks + a.chunk_begin[s]) * kItemFloats;
+    const int first = (h * a.total_chunks + a.chunk_begin[s]) * kItemFloats * 4;
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k0 = 0; k0 < n_chunks; k0 += kCombineBatch) {
-        f32x4 av[kCombineBatch];
-        float2 ml[kCombineBatch];
+        u32x4 pa[kCombineBatch];
+        u32x2 pm[kCombineBatch];
 #pragma unroll
         for (int k = 0; k < kCombineBatch; k++) {
             const int kk = min(k0 + k, n_chunks - 1);
-            const float* pk = first + (size_t)kk * kItemFloats;
-            av[k] = *reinterpret_cast<const f32x4*>(pk + g * kHeadDim + d0);
-            ml[k] = *reinterpret_cast<const float2*>(pk + kGroup * kHeadDim + 2 * g);
+            const int kb = first + kk * kItemFloats * 4;
+            pa[k] = __builtin_amdgcn_raw_buffer_load_b128(prs, kb + (g * kHeadDim + d0) * 4, 0, kCpolSC1);
+            pm[k] = __builtin_amdgcn_raw_buffer_load_b64(prs, kb + (kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
         }
         float mb = Mc;
 #pragma unroll
         for (int k = 0; k < kCombineBatch; k++)
-            if (k0 + k < n_chunks) mb = fmaxf(mb, ml[k].x);
+            if (k0 + k < n_chunks) mb = fmaxf(mb, __uint_as_float(pm[k][0]));
         const float cc = fast_exp2(Mc - mb);
         Lc *= cc;
         Ac[0] *= cc; Ac[1] *= cc; Ac[2] *= cc; Ac[3] *= cc;
         Mc = mb;
 #pragma unroll
         for (int k = 0; k < kCombineBatch; k++) {
-            const float w = (k0 + k < n_chunks) ? fast_exp2(ml[k].x - Mc) : 0.f;
-            Lc = fmaf(w, ml[k].y, Lc);
-            Ac[0] = fmaf(w, av[k][0], Ac[0]);
-            Ac[1] = fmaf(w, av[k][1], Ac[1]);
-            Ac[2] = fmaf(w, av[k][2], Ac[2]);
-            Ac[3] = fmaf(w, av[k][3], Ac[3]);
+            const float w = (k0 + k < n_chunks) ? fast_exp2(__uint_as_float(pm[k][0]) - Mc) : 0.f;
+            Lc = fmaf(w, __uint_as_float(pm[k][1]), Lc);
+            Ac[0] = fmaf(w, __uint_as_float(pa[k][0]), Ac[0]);
+            Ac[1] = fmaf(w, __uint_as_float(pa[k][1]), Ac[1]);
+            Ac[2] = fmaf(w, __uint_as_float(pa[k][2]), Ac[2]);
+            Ac[3] = fmaf(w, __uint_as_float(pa[k][3]), Ac[3]);
         }
     }
     write_out(a.out, a.out_bf16, orow, d0, grow, Lc, Ac);

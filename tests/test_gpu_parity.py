@@ -242,3 +242,33 @@ def test_prefill_batch_vs_oracle():
             ref = O.prefill_attn(q[i], mk, mv, P, n)
             O.assert_attn_close(out[i], ref, what=f"prefill P={P}")
             O.assert_attn_close(out[i], ref, rel_rms=3e-3, what='tight')
+
+
+def test_splitk_workspace_reuse_stress():
+    """Many split-K launches back to back on one stream, each with new data in
+    the same partial workspace and arrival counters: every output must match
+    the oracle (catches stale partials read across XCDs)."""
+    say("split-K workspace reuse stress")
+    lens = [4096, 700, 1537]
+    with make_ctx(decode_chunk_blocks=1) as ctx:
+        m = Mirror(1)
+        seqs = [ctx.seq_create() for _ in lens]
+        for s, L in zip(seqs, lens):
+            fill_seq(ctx, m, [s], L, seed=9100 + L, layers=[0])
+        h = kvc.hip()
+        n = len(seqs)
+        reps = 12
+        qs = O.normal_bf16(reps * n * NQ * D, 9200).reshape(reps, n, NQ, D)
+        qb = h.malloc(qs.nbytes).upload(qs)
+        ob = h.malloc(reps * n * NQ * D * 4)
+        for r in range(reps):
+            ctx.decode_attn(0, seqs, qb.ptr + r * n * NQ * D * 2, ob.ptr + r * n * NQ * D * 4)
+        ctx.sync()
+        out = ob.download(np.float32, (reps, n, NQ, D))
+        qb.free()
+        ob.free()
+        for r in range(reps):
+            for i, (s, L) in enumerate(zip(seqs, lens)):
+                mk, mv = m.get(s, 0)
+                ref = O.decode_attn(qs[r, i], mk, mv, L)
+                O.assert_attn_close(out[r, i], ref, rel_rms=3e-3, what=f"rep {r} L={L}")
