@@ -915,9 +915,11 @@ int kvc_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
 
 static int32_t auto_chunk_blocks(kvc_ctx* c, int64_t total_blocks) {
     if (c->cfg.decode_chunk_blocks > 0) return c->cfg.decode_chunk_blocks;
-    const int64_t target_items = 2048;  // ~8 workgroups per CU on 256 CUs
+    // ~4 workgroups per CU on 256 CUs; chunks of at least 4 blocks keep the
+    // split-K partial traffic and the final combine small
+    const int64_t target_items = 1024;
     int64_t cb = (total_blocks * kKvHeads + target_items - 1) / target_items;
-    return (int32_t)std::max<int64_t>(2, cb);
+    return (int32_t)std::max<int64_t>(4, cb);
 }
 
 int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q, const void* k_new,
@@ -1031,7 +1033,7 @@ int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
         const int32_t n = std::min(kMaxBatch, n_seqs - i0);
         GatherArgs a{};
-        int64_t tot = 0;
+        int64_t tot = 0, items = 0;
         for (int32_t j = 0; j < n; j++) {
             const Seq& s = c->seqs[seqs[i0 + j]];
             const int32_t nt = n_tok[i0 + j];
@@ -1040,9 +1042,13 @@ int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
                                tok0 + nt, s.len + s.pending);
             a.slot[j] = seqs[i0 + j];
             a.out_begin[j] = (int32_t)tot;
+            a.item_begin[j] = (int32_t)items;
             tot += nt;
+            items += (nt + kBlockTok - 1) / kBlockTok;
         }
         a.out_begin[n] = (int32_t)tot;
+        a.item_begin[n] = (int32_t)items;
+        a.n_items = (int32_t)items;
         if (tot * kKvHeads * 2 * (kHeadDim * 2 / 16) > (int64_t)UINT32_MAX * 256)
             return set_err(KVC_ERR_RANGE, "gather too large");
         a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);

@@ -97,8 +97,11 @@ struct GatherArgs {
     int32_t n_seqs;
     int32_t tok0;
     int32_t total_tok;
+    int32_t n_items;                    // (seq, 32-token output chunk) work items
+    int32_t pad;
     int32_t slot[kMaxBatch];
-    int32_t out_begin[kMaxBatch + 1];  // token offsets into the packed output
+    int32_t out_begin[kMaxBatch + 1];   // token offsets into the packed output
+    int32_t item_begin[kMaxBatch + 1];  // first work item of each sequence
 };
 
 struct PrefillArgs {

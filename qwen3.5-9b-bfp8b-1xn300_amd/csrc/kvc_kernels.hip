@@ -420,7 +420,7 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
 // the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8).  Each item
 // writes (m, l, acc) for its 4 q heads; the last item of a (seq, head) to
 // arrive (device-scope counter) combines them and writes the output.
-constexpr int kCombineBatch = 16;
+constexpr int kCombineBatch = 8;
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     __shared__ DecodeSmem sm;
@@ -497,67 +497,269 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
     if (!sm.last) return;
-    // combine the n_chunks partials of (s, h); loads of a batch are all issued
-    // before any is used
+    // combine the n_chunks partials of (s, h) in batches; the next batch's
+    // loads are issued before the current batch is reduced
     const int first = (h * a.total_chunks + a.chunk_begin[s]) * kItemFloats * 4;
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < n_chunks; k0 += kCombineBatch) {
-        u32x4 pa[kCombineBatch];
-        u32x2 pm[kCombineBatch];
+    u32x4 pa[2][kCombineBatch];
+    u32x2 pm[2][kCombineBatch];
+    auto fetch = [&](int buf, int k0) {
 #pragma unroll
         for (int k = 0; k < kCombineBatch; k++) {
-            const int kk = min(k0 + k, n_chunks - 1);
-            const int kb = first + kk * kItemFloats * 4;
-            pa[k] = __builtin_amdgcn_raw_buffer_load_b128(prs, kb + (g * kHeadDim + d0) * 4, 0, kCpolSC1);
-            pm[k] = __builtin_amdgcn_raw_buffer_load_b64(prs, kb + (kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
+            const int kb = first + min(k0 + k, n_chunks - 1) * kItemFloats * 4;
+            pa[buf][k] = __builtin_amdgcn_raw_buffer_load_b128(prs, kb + (g * kHeadDim + d0) * 4, 0, kCpolSC1);
+            pm[buf][k] = __builtin_amdgcn_raw_buffer_load_b64(prs, kb + (kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
         }
+    };
+    auto reduce = [&](int buf, int k0) {
         float mb = Mc;
 #pragma unroll
         for (int k = 0; k < kCombineBatch; k++)
-            if (k0 + k < n_chunks) mb = fmaxf(mb, __uint_as_float(pm[k][0]));
+            if (k0 + k < n_chunks) mb = fmaxf(mb, __uint_as_float(pm[buf][k][0]));
         const float cc = fast_exp2(Mc - mb);
         Lc *= cc;
         Ac[0] *= cc; Ac[1] *= cc; Ac[2] *= cc; Ac[3] *= cc;
         Mc = mb;
 #pragma unroll
         for (int k = 0; k < kCombineBatch; k++) {
-            const float w = (k0 + k < n_chunks) ? fast_exp2(__uint_as_float(pm[k][0]) - Mc) : 0.f;
-            Lc = fmaf(w, __uint_as_float(pm[k][1]), Lc);
-            Ac[0] = fmaf(w, __uint_as_float(pa[k][0]), Ac[0]);
-            Ac[1] = fmaf(w, __uint_as_float(pa[k][1]), Ac[1]);
-            Ac[2] = fmaf(w, __uint_as_float(pa[k][2]), Ac[2]);
-            Ac[3] = fmaf(w, __uint_as_float(pa[k][3]), Ac[3]);
+            const float w = (k0 + k < n_chunks) ? fast_exp2(__uint_as_float(pm[buf][k][0]) - Mc) : 0.f;
+            Lc = fmaf(w, __uint_as_float(pm[buf][k][1]), Lc);
+            Ac[0] = fmaf(w, __uint_as_float(pa[buf][k][0]), Ac[0]);
+            Ac[1] = fmaf(w, __uint_as_float(pa[buf][k][1]), Ac[1]);
+            Ac[2] = fmaf(w, __uint_as_float(pa[buf][k][2]), Ac[2]);
+            Ac[3] = fmaf(w, __uint_as_float(pa[buf][k][3]), Ac[3]);
         }
+    };
+    fetch(0, 0);
+    for (int k0 = 0; k0 < n_chunks; k0 += 2 * kCombineBatch) {
+        if (k0 + kCombineBatch < n_chunks) fetch(1, k0 + kCombineBatch);
+        reduce(0, k0);
+        if (k0 + kCombineBatch >= n_chunks) break;
+        if (k0 + 2 * kCombineBatch < n_chunks) fetch(0, k0 + 2 * kCombineBatch);
+        reduce(1, k0 + kCombineBatch);
     }
     write_out(a.out, a.out_bf16, orow, d0, grow, Lc, Ac);
     if (t == 0) a.counters[s * kKvHeads + h] = 0;
 }
 
 // ---------------------------------------------------------------------------
-// Causal prefill, one workgroup per (seq, query row, kv head); row r of seq s
-// sits at position q_pos0[s] + r and reads keys [0, pos].
-__global__ __launch_bounds__(kThreads) void prefill_rowwise_kernel(PrefillArgs a) {
-    __shared__ DecodeSmem sm;
-    const int h = blockIdx.x % kKvHeads;
-    const int row = (blockIdx.x / kKvHeads) % a.n_q;
-    const int s = blockIdx.x / (kKvHeads * a.n_q);
-    const int L = a.q_pos0[s] + row + 1;
-    const int n_blocks = (L + kBlockTok - 1) / kBlockTok;
-    const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t qrow = (((size_t)s * a.n_q + row) * kQHeads + h * kGroup) * kHeadDim;
+// Causal chunked prefill with bf16 MFMA (v_mfma_f32_16x16x32_bf16).
+//
+// Workgroup = (sequence, kv head, 32 consecutive query positions); wave g
+// handles q head g of the GQA group, so each 64-key K/V tile staged in LDS
+// serves 4 q heads.  Per tile and wave:
+//   S^T[64 keys x 32 rows]  = K[keys x 256] . Q^T          (A = K from LDS)
+//   P^T = 2^(S^T - m)       (online softmax, log2 domain, bf16)
+//   O^T[256 d x 32 rows]   += V^T[d x keys] . P^T          (A = V^T from LDS)
+// Working on transposes keeps each lane on one query row (row = lane % 16)
+// in both products, so the row statistics need no lane shuffles and P^T
+// leaves the S^T accumulator already in B-operand order.  Keys inside one
+// 32-key MFMA step are taken in the order (4q + i, 16 + 4q + i) for lane group
+// q = lane / 16, i = 0..3, on both operands (a consistent permutation of the
+// summation index).  K is staged row-major, V transposed (ds_write_b16); the
+// next tile's global loads are issued before the current tile is computed.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+constexpr int kPfRows = 32;                 // query positions per workgroup
+constexpr int kPfKeys = 64;                 // keys per tile
+constexpr int kKStride = kHeadDim + 8;      // K tile row stride (elements), 528 B
+constexpr int kVtStride = kPfKeys + 4;      // V^T tile row stride (elements), 136 B
 
-    uint32_t qv[kGroup][2][4];
-    load_q(qv, a.q + qrow, lane);
-    WaveState st;
-    init_state(st);
-    walk_blocks(a.kpool, a.vpool, trow, h, 0, n_blocks, L, qv, a.scale_log2, sm.p16[wave], st, wave, lane);
-    finalize_l(st);
-    float M, Lsum, A[4];
-    merge_waves(st, sm, wave, lane, M, Lsum, A);
-    const int t = threadIdx.x, g = t >> 6, d0 = (t & 63) * 4;
-    const size_t orow = qrow + (size_t)g * kHeadDim;
-    write_out(a.out, a.out_bf16, orow, d0, a.gate ? a.gate + orow : nullptr, Lsum, A);
+struct PrefillSmem {
+    uint16_t k[kPfKeys * kKStride];
+    uint16_t vt[kHeadDim * kVtStride];
+};
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void prefill_mfma_kernel(PrefillArgs a) {
+    __shared__ PrefillSmem sm;
+    const int n_pb = (a.n_q + kPfRows - 1) / kPfRows;
+    const int pb = blockIdx.x % n_pb;
+    const int h = (blockIdx.x / n_pb) % kKvHeads;
+    const int s = blockIdx.x / (n_pb * kKvHeads);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int q4 = lane >> 4, r16 = lane & 15;
+    const int g = wave;
+    const int pos0 = a.q_pos0[s];
+    const int row0 = pb * kPfRows;                     // first query row of the tile
+    const int rows = min(kPfRows, a.n_q - row0);
+    const int kmax = pos0 + row0 + rows;               // keys [0, kmax) are visible
+    const int n_tiles = (kmax + kPfKeys - 1) / kPfKeys;
+    const int n_blocks = (kmax + kBlockTok - 1) / kBlockTok;
+    const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
+    constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
+
+    // Q^T as the B operand: qb[nt][ks] = q[row 16nt + r16][d 32ks + 8q4 .. +7]
+    bf16x8_t qb[2][8];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        const int r = row0 + min(16 * nt + r16, rows - 1);
+        const uint16_t* qr = a.q + (((size_t)s * a.n_q + r) * kQHeads + h * kGroup + g) * kHeadDim;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            qb[nt][ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * q4));
+    }
+
+    // global -> register staging of one tile: thread owns 16-B pieces
+    // u = j*256 + tid (j = 0..7) of the 64 x 256 K and V tiles
+    u32x4 kst[8], vst[8];
+    auto fetch_tile = [&](int t) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int u = j * 256 + tid;
+            const int key = t * kPfKeys + (u >> 5);
+            const int col = (u & 31) * 8;
+            const int blk = min(key / kBlockTok, n_blocks - 1);
+            const size_t off = ((size_t)trow[blk] * kKvHeads + h) * kUnitElems + (key % kBlockTok) * kHeadDim + col;
+            kst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kpool + off));
+            vst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vpool + off));
+        }
+    };
+
+    f32x4 o[16][2];
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) o[dt][0] = o[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {kNegBig, kNegBig};
+    float l_lane[2] = {0.f, 0.f};
+
+    fetch_tile(0);
+    for (int t = 0; t < n_tiles; t++) {
+        __syncthreads();  // previous tile's LDS reads are done
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int u = j * 256 + tid;
+            const int key = u >> 5, col = (u & 31) * 8;
+            *reinterpret_cast<u32x4*>(&sm.k[key * kKStride + col]) = kst[j];
+            const u32x4 v = vst[j];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                sm.vt[(col + 2 * e) * kVtStride + key] = (uint16_t)(v[e] & 0xFFFFu);
+                sm.vt[(col + 2 * e + 1) * kVtStride + key] = (uint16_t)(v[e] >> 16);
+            }
+        }
+        __syncthreads();
+        if (t + 1 < n_tiles) fetch_tile(t + 1);
+
+        // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16
+        f32x4 st[4][2];
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++) {
+            st[kt][0] = st[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                const bf16x8_t ka = as_bf16x8(
+                    *reinterpret_cast<const u32x4*>(&sm.k[(16 * kt + r16) * kKStride + 32 * ks + 8 * q4]));
+                st[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[0][ks], st[kt][0], 0, 0, 0);
+                st[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[1][ks], st[kt][1], 0, 0, 0);
+            }
+        }
+        // scale, causal mask, online softmax (lazy rescale with slack)
+        bool need = false;
+        float mt[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+            const int qpos = pos0 + row0 + 16 * nt + r16;
+            float mx = kNegBig;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int kp = t * kPfKeys + 16 * kt + 4 * q4 + i;
+                    const float v = (kp <= qpos && kp < kmax) ? st[kt][nt][i] * a.scale_log2 : kNegBig;
+                    st[kt][nt][i] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = max_xor16(mx);
+            mx = max_xor32(mx);
+            mt[nt] = mx;
+            need |= mx > m_run[nt] + kRescaleSlack;
+        }
+        if (__builtin_amdgcn_ballot_w64(need) != 0) {
+#pragma unroll
+            for (int nt = 0; nt < 2; nt++) {
+                if (mt[nt] > m_run[nt] + kRescaleSlack) {
+                    const float c = fast_exp2(m_run[nt] - mt[nt]);
+                    m_run[nt] = mt[nt];
+                    l_lane[nt] *= c;
+#pragma unroll
+                    for (int dt = 0; dt < 16; dt++) o[dt][nt] *= c;
+                }
+            }
+        }
+        // P^T as the B operand (bf16), k-slot order (4q4 + i, 16 + 4q4 + i)
+        bf16x8_t pb_[2][2];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++) {
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                u32x4 w;
+#pragma unroll
+                for (int half = 0; half < 2; half++) {
+                    const f32x4 sv = st[2 * kk + half][nt];
+                    float p[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        p[i] = bf16_round(fast_exp2(sv[i] - m_run[nt]));
+                        l_lane[nt] += p[i];
+                    }
+                    w[2 * half] = (__float_as_uint(p[0]) >> 16) | (__float_as_uint(p[1]) & 0xFFFF0000u);
+                    w[2 * half + 1] = (__float_as_uint(p[2]) >> 16) | (__float_as_uint(p[3]) & 0xFFFF0000u);
+                }
+                pb_[nt][kk] = as_bf16x8(w);
+            }
+        }
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                const uint16_t* vr = &sm.vt[(16 * dt + r16) * kVtStride + 32 * kk + 4 * q4];
+                const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
+                const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 16);
+                u32x4 w;
+                w[0] = lo[0];
+                w[1] = lo[1];
+                w[2] = hi[0];
+                w[3] = hi[1];
+                const bf16x8_t va = as_bf16x8(w);
+                o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[0][kk], o[dt][0], 0, 0, 0);
+                o[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[1][kk], o[dt][1], 0, 0, 0);
+            }
+        }
+    }
+    // epilogue: row sums across the 4 lane groups, normalise, gate, store
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        float l = l_lane[nt];
+        l = sum_xor16(l);
+        l = sum_xor32(l);
+        const int rl = 16 * nt + r16;
+        if (rl >= rows) continue;
+        const size_t orow = (((size_t)s * a.n_q + row0 + rl) * kQHeads + h * kGroup + g) * kHeadDim;
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+            const int d0 = 16 * dt + 4 * q4;
+            float v4[4] = {o[dt][nt][0] * inv, o[dt][nt][1] * inv, o[dt][nt][2] * inv, o[dt][nt][3] * inv};
+            if (a.gate) {
+                const uint2 gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+                v4[0] *= sigmoidf_exact(bf16lo(gw.x));
+                v4[1] *= sigmoidf_exact(bf16hi(gw.x));
+                v4[2] *= sigmoidf_exact(bf16lo(gw.y));
+                v4[3] *= sigmoidf_exact(bf16hi(gw.y));
+            }
+            if (a.out_bf16) {
+                uint2 w;
+                w.x = pack_bf16x2(v4[0], v4[1]);
+                w.y = pack_bf16x2(v4[2], v4[3]);
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + orow + d0) = w;
+            } else {
+                *reinterpret_cast<float4*>(static_cast<float*>(a.out) + orow + d0) =
+                    make_float4(v4[0], v4[1], v4[2], v4[3]);
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -583,27 +785,44 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a, int n_units) 
     *reinterpret_cast<uint4*>(to + dst) = *reinterpret_cast<const uint4*>(from + src);
 }
 
-// Gather: packed output rows [tok][head][d]; one thread per 16 B of K or V.
+// Gather: workgroup = (sequence, 32 consecutive output tokens); output rows
+// are [tok][kv_head][d] packed back to back.  Each thread moves 16 x 16 B of K
+// then of V, all loads issued before the stores.
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
-    const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    constexpr int kRowUnits = kHeadDim * 2 / 16;
-    const int64_t rows = (int64_t)a.total_tok * kKvHeads;
-    if (u >= 2 * rows * kRowUnits) return;
-    const int part = (int)(u % kRowUnits);
-    const int64_t row = u / kRowUnits;
-    const int kv = row >= rows;
-    const int64_t r = row - (kv ? rows : 0);
-    const int h = (int)(r % kKvHeads);
-    const int otok = (int)(r / kKvHeads);
+    const int item = blockIdx.x;
     int s = 0;
-    while (s + 1 < a.n_seqs && a.out_begin[s + 1] <= otok) s++;
-    const int pos = a.tok0 + otok - a.out_begin[s];
-    const int blk = a.table[(size_t)a.slot[s] * a.table_stride + pos / kBlockTok];
-    const size_t src = (((size_t)blk * kKvHeads + h) * kBlockTok + pos % kBlockTok) * kHeadDim + part * 8;
-    const uint16_t* from = kv ? a.vpool : a.kpool;
-    uint16_t* to = kv ? a.v_out : a.k_out;
-    *reinterpret_cast<u32x4*>(to + r * kHeadDim + part * 8) =
-        __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(from + src));
+    while (s + 1 < a.n_seqs && a.item_begin[s + 1] <= item) s++;
+    const int c = item - a.item_begin[s];
+    const int n_tok = a.out_begin[s + 1] - a.out_begin[s];
+    const int t0 = c * kBlockTok;
+    const int nt = min(kBlockTok, n_tok - t0);
+    const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
+    constexpr int kRowUnits = kHeadDim * 2 / 16;           // 32 x 16 B per row
+    constexpr int kUnits = kBlockTok * kKvHeads * kRowUnits;  // 4096 per tensor
+    constexpr int kPer = kUnits / 256;                      // 16 per thread
+#pragma unroll
+    for (int kv = 0; kv < 2; kv++) {
+        const uint16_t* pool = kv ? a.vpool : a.kpool;
+        uint16_t* outp = (kv ? a.v_out : a.k_out) + ((size_t)a.out_begin[s] + t0) * kKvHeads * kHeadDim;
+        u32x4 buf[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const int u = j * 256 + threadIdx.x;
+            const int tok = u / (kKvHeads * kRowUnits);
+            const int hh = (u / kRowUnits) % kKvHeads;
+            const int part = u % kRowUnits;
+            const int pos = a.tok0 + t0 + min(tok, nt - 1);
+            const size_t src = (((size_t)trow[pos / kBlockTok] * kKvHeads + hh) * kBlockTok + pos % kBlockTok) *
+                                   kHeadDim + part * 8;
+            buf[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pool + src));
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; j++) {
+            const int u = j * 256 + threadIdx.x;
+            if (u / (kKvHeads * kRowUnits) < nt)
+                __builtin_nontemporal_store(buf[j], reinterpret_cast<u32x4*>(outp + (size_t)u * 8));
+        }
+    }
 }
 
 // Snapshot save/restore: per pair, the sequence's whole recurrent state then
@@ -713,8 +932,8 @@ int launch_decode(const DecodeArgs& a, void* stream) {
 }
 
 int launch_prefill(const PrefillArgs& a, void* stream) {
-    const int grid = a.n_seqs * a.n_q * kKvHeads;
-    hipLaunchKernelGGL(prefill_rowwise_kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a);
+    const int grid = a.n_seqs * kKvHeads * ((a.n_q + kPfRows - 1) / kPfRows);
+    hipLaunchKernelGGL(prefill_mfma_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
@@ -725,9 +944,8 @@ int launch_append(const AppendArgs& a, int n_units, void* stream) {
 }
 
 int launch_gather(const GatherArgs& a, void* stream) {
-    const int64_t units = (int64_t)a.total_tok * kKvHeads * 2 * (kHeadDim * 2 / 16);
-    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
-                       (hipStream_t)stream, a);
+    if (a.n_items <= 0) return 0;
+    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)a.n_items), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 

@@ -272,3 +272,38 @@ def test_splitk_workspace_reuse_stress():
                 mk, mv = m.get(s, 0)
                 ref = O.decode_attn(qs[r, i], mk, mv, L)
                 O.assert_attn_close(out[r, i], ref, rel_rms=3e-3, what=f"rep {r} L={L}")
+
+
+def test_prefill_long_prefix_gate_bf16():
+    """Config-c shape: 128-row causal chunk over a ~2.9K-token prefix, with
+    gate and bf16 output, one session per kv-head tiling edge case."""
+    say("prefill long prefix, gate, bf16 out")
+    prefixes = [2900, 37]
+    n = 128
+    with make_ctx() as ctx:
+        m = Mirror(1)
+        h = kvc.hip()
+        seqs = [ctx.seq_create() for _ in prefixes]
+        for s, P in zip(seqs, prefixes):
+            fill_seq(ctx, m, [s], P, seed=8000 + P, layers=[0], chunk=1024)
+        ns = len(seqs)
+        k = O.normal_bf16(ns * n * ROW, 801).reshape(ns, n, ROW)
+        v = O.normal_bf16(ns * n * ROW, 802).reshape(ns, n, ROW)
+        q = O.normal_bf16(ns * n * NQ * D, 803).reshape(ns, n, NQ, D)
+        gt = O.normal_bf16(ns * n * NQ * D, 804).reshape(ns, n, NQ, D)
+        ctx.reserve(seqs, n)
+        bufs = [h.malloc(x.nbytes).upload(x) for x in (k, v, q, gt)]
+        ob = h.malloc(ns * n * NQ * D * 2)
+        ctx.append(0, seqs, n, bufs[0], bufs[1])
+        ctx.prefill_attn(0, seqs, n, bufs[2], ob, gate=bufs[3], out_dtype=kvc.DTYPE_BF16)
+        ctx.commit(seqs, n)
+        ctx.sync()
+        out = O.bf16_to_f32(ob.download(np.uint16, (ns, n, NQ, D)))
+        for b in bufs + [ob]:
+            b.free()
+        for i, (s, P) in enumerate(zip(seqs, prefixes)):
+            m.append(s, 0, k[i], v[i])
+            mk, mv = m.get(s, 0)
+            ref = O.prefill_attn(q[i], mk, mv, P, n, gate=gt[i])
+            O.assert_attn_close(out[i], ref, what=f"prefill P={P}")
+            O.assert_attn_close(out[i], ref, rel_rms=5e-3, what=f"prefill P={P} tight")
