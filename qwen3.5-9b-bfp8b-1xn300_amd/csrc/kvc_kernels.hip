@@ -105,7 +105,8 @@ __device__ __forceinline__ float max_xor32(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(f32_to_bf16_rne(x) << 16); }
+// x rounded to bf16 (RNE) and widened back; x finite.
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(cvt_pk_bf16(x, 0.f) << 16); }
 
 // Scores, online softmax update and P.V for one block held in registers.
 // qv[g][j][i]: packed bf16 pairs of q head g, dims (c + 16j)*8 + 2i, +1.
@@ -286,12 +287,16 @@ __device__ __forceinline__ void merge_waves(const WaveState& st, DecodeSmem& sm,
     }
 }
 
-__device__ __forceinline__ float sigmoidf_exact(float x) { return 1.0f / (1.0f + __expf(-x)); }
+// sigmoid to within a few ulp: v_exp_f32 and v_rcp_f32 (the reference uses
+// a Schraudolph approximation with ~4% exp error, src/engine.cpp:2349-2360)
+__device__ __forceinline__ float sigmoidf_exact(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-x * 1.4426950408889634f));
+}
 
 // out row = A / L (* sigmoid(gate)), written as bf16 (RNE) or fp32.
 __device__ __forceinline__ void write_out(void* out, int out_bf16, size_t row_off, int d0,
                                           const uint16_t* gate_row, float L, const float (&A)[4]) {
-    const float inv = 1.0f / L;
+    const float inv = __builtin_amdgcn_rcpf(L);
     float o[4] = {A[0] * inv, A[1] * inv, A[2] * inv, A[3] * inv};
     if (gate_row) {
         const uint2 gw = *reinterpret_cast<const uint2*>(gate_row + d0);
@@ -548,28 +553,37 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
 // Workgroup = (sequence, kv head, 32 consecutive query positions); wave g
 // handles q head g of the GQA group, so each 64-key K/V tile staged in LDS
 // serves 4 q heads.  Per tile and wave:
-//   S^T[64 keys x 32 rows]  = K[keys x 256] . Q^T          (A = K from LDS)
+//   S^T[64 keys x 32 rows]  = K[keys x 256] . Q^T          (A = K rows, LDS)
 //   P^T = 2^(S^T - m)       (online softmax, log2 domain, bf16)
-//   O^T[256 d x 32 rows]   += V^T[d x keys] . P^T          (A = V^T from LDS)
+//   O^T[256 d x 32 rows]   += V^T[d x keys] . P^T          (A = V^T, LDS)
 // Working on transposes keeps each lane on one query row (row = lane % 16)
 // in both products, so the row statistics need no lane shuffles and P^T
 // leaves the S^T accumulator already in B-operand order.  Keys inside one
 // 32-key MFMA step are taken in the order (4q + i, 16 + 4q + i) for lane group
 // q = lane / 16, i = 0..3, on both operands (a consistent permutation of the
-// summation index).  K is staged row-major, V transposed (ds_write_b16); the
-// next tile's global loads are issued before the current tile is computed.
+// summation index).  K and V tiles are staged row-major (token rows, 16-B
+// writes); the V^T operand is read with ds_read_b64_tr_b16, which hands lane
+// i of each 16-lane group element i%4 of the 8-B pieces addressed by lanes
+// i/4, 4 + i/4, 8 + i/4, 12 + i/4 -- a 4 x 16 transpose.  The next tile's
+// global loads are issued before the current tile is computed.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
 constexpr int kPfRows = 32;                 // query positions per workgroup
 constexpr int kPfKeys = 64;                 // keys per tile
-constexpr int kKStride = kHeadDim + 8;      // K tile row stride (elements), 528 B
-constexpr int kVtStride = kPfKeys + 4;      // V^T tile row stride (elements), 136 B
+constexpr int kKStride = kHeadDim + 8;      // K / V tile row stride (elements), 528 B
 
 struct PrefillSmem {
     uint16_t k[kPfKeys * kKStride];
-    uint16_t vt[kHeadDim * kVtStride];
+    uint16_t v[kPfKeys * kKStride];
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+    const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (i16x4_t __attribute__((address_space(3)))*)(p));
+    return __builtin_bit_cast(u32x2, r);
+}
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_mfma_kernel(PrefillArgs a) {
@@ -601,17 +615,22 @@ void prefill_mfma_kernel(PrefillArgs a) {
             qb[nt][ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * q4));
     }
 
+    // block ids of a 64-block window sit in one VGPR (lane i = block w0 + i)
+    // and are read with v_readlane: no dependent table load on the fetch path
+    int idw0 = 0;
+    int idv = lane < n_blocks ? trow[lane] : 0;
     // global -> register staging of one tile: thread owns 16-B pieces
-    // u = j*256 + tid (j = 0..7) of the 64 x 256 K and V tiles
+    // u = j*256 + tid (j = 0..7) of the 64 x 256 K and V token rows
     u32x4 kst[8], vst[8];
     auto fetch_tile = [&](int t) {
+        const int b0 = min(2 * t, n_blocks - 1), b1 = min(2 * t + 1, n_blocks - 1);
+        const size_t u0 = ((size_t)__builtin_amdgcn_readlane(idv, b0 - idw0) * kKvHeads + h) * kUnitElems;
+        const size_t u1 = ((size_t)__builtin_amdgcn_readlane(idv, b1 - idw0) * kKvHeads + h) * kUnitElems;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int u = j * 256 + tid;
-            const int key = t * kPfKeys + (u >> 5);
-            const int col = (u & 31) * 8;
-            const int blk = min(key / kBlockTok, n_blocks - 1);
-            const size_t off = ((size_t)trow[blk] * kKvHeads + h) * kUnitElems + (key % kBlockTok) * kHeadDim + col;
+            const int key = u >> 5;  // 0..63 within the tile; j < 4 -> first block
+            const size_t off = (j < 4 ? u0 : u1) + (key % kBlockTok) * kHeadDim + (u & 31) * 8;
             kst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kpool + off));
             vst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vpool + off));
         }
@@ -630,16 +649,21 @@ void prefill_mfma_kernel(PrefillArgs a) {
         for (int j = 0; j < 8; j++) {
             const int u = j * 256 + tid;
             const int key = u >> 5, col = (u & 31) * 8;
-            *reinterpret_cast<u32x4*>(&sm.k[key * kKStride + col]) = kst[j];
-            const u32x4 v = vst[j];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                sm.vt[(col + 2 * e) * kVtStride + key] = (uint16_t)(v[e] & 0xFFFFu);
-                sm.vt[(col + 2 * e + 1) * kVtStride + key] = (uint16_t)(v[e] >> 16);
-            }
+            // keys past the sequence end come from stale slots: zero them so
+            // no NaN bit pattern reaches the MFMA (their p is 0 already)
+            const bool live = t * kPfKeys + key < kmax;
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4*>(&sm.k[key * kKStride + col]) = live ? kst[j] : z;
+            *reinterpret_cast<u32x4*>(&sm.v[key * kKStride + col]) = live ? vst[j] : z;
         }
         __syncthreads();
-        if (t + 1 < n_tiles) fetch_tile(t + 1);
+        if (t + 1 < n_tiles) {
+            if (2 * (t + 1) + 1 - idw0 >= 64 && 2 * (t + 1) < n_blocks) {  // uniform: next id window
+                idw0 = 2 * (t + 1);
+                idv = idw0 + lane < n_blocks ? trow[idw0 + lane] : 0;
+            }
+            fetch_tile(t + 1);
+        }
 
         // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16
         f32x4 st[4][2];
@@ -697,26 +721,26 @@ void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int half = 0; half < 2; half++) {
                     const f32x4 sv = st[2 * kk + half][nt];
-                    float p[4];
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        p[i] = bf16_round(fast_exp2(sv[i] - m_run[nt]));
-                        l_lane[nt] += p[i];
-                    }
-                    w[2 * half] = (__float_as_uint(p[0]) >> 16) | (__float_as_uint(p[1]) & 0xFFFF0000u);
-                    w[2 * half + 1] = (__float_as_uint(p[2]) >> 16) | (__float_as_uint(p[3]) & 0xFFFF0000u);
+                    const uint32_t w0 = cvt_pk_bf16(fast_exp2(sv[0] - m_run[nt]), fast_exp2(sv[1] - m_run[nt]));
+                    const uint32_t w1 = cvt_pk_bf16(fast_exp2(sv[2] - m_run[nt]), fast_exp2(sv[3] - m_run[nt]));
+                    // the denominator sums the same rounded weights
+                    l_lane[nt] += (bf16lo(w0) + bf16hi(w0)) + (bf16lo(w1) + bf16hi(w1));
+                    w[2 * half] = w0;
+                    w[2 * half + 1] = w1;
                 }
                 pb_[nt][kk] = as_bf16x8(w);
             }
         }
-        // O^T += V^T . P^T
+        // O^T += V^T . P^T; the V^T operand of lane (q4, r16) is V[keys
+        // 32kk + 4q4 + e (+16)][16dt + r16]: lane J of the group addresses
+        // row 32kk + 4q4 + J/4 (+16), dims 16dt + 4(J%4) .. +3
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) {
 #pragma unroll
             for (int kk = 0; kk < 2; kk++) {
-                const uint16_t* vr = &sm.vt[(16 * dt + r16) * kVtStride + 32 * kk + 4 * q4];
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 16);
+                const uint16_t* vp = &sm.v[(32 * kk + 4 * q4 + (r16 >> 2)) * kKStride + 16 * dt + 4 * (r16 & 3)];
+                const u32x2 lo = lds_read_tr16(vp);
+                const u32x2 hi = lds_read_tr16(vp + 16 * kKStride);
                 u32x4 w;
                 w[0] = lo[0];
                 w[1] = lo[1];
@@ -737,7 +761,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
         const int rl = 16 * nt + r16;
         if (rl >= rows) continue;
         const size_t orow = (((size_t)s * a.n_q + row0 + rl) * kQHeads + h * kGroup + g) * kHeadDim;
-        const float inv = 1.0f / l;
+        const float inv = __builtin_amdgcn_rcpf(l);
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) {
             const int d0 = 16 * dt + 4 * q4;
