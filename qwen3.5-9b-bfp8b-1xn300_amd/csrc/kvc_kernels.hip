@@ -9,8 +9,7 @@
 
 namespace kvc {
 
-constexpr int kWaves = 4;           // waves per decode workgroup
-constexpr int kThreads = kWaves * 64;
+constexpr int kWaves = 4;           // waves per decode workgroup (each takes 8 tokens of a block)
 constexpr int kTokPerWave = kBlockTok / kWaves;  // 8 tokens of a block per wave
 constexpr float kNegBig = -1.0e30f;
 constexpr float kRescaleSlack = 8.0f;  // lazy rescale: p may reach 2^8
@@ -333,49 +332,63 @@ __device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpoo
 }
 
 // ---------------------------------------------------------------------------
-// Walk blocks [blk0, blk1) of one (sequence, kv head) with two register
-// buffers (the next block's loads are in flight while the current one is
-// computed).  Block ids are fetched once per 64 blocks into a VGPR and read
-// back per block with v_readlane, so no table load sits on the critical path.
-// Walk blocks [blk0, blk1) of one (sequence, kv head); keys at positions >= L
-// are masked.  Block ids are fetched once per 64 blocks into a VGPR and read
-// back per block with v_readlane, so no table load sits in the pipeline.
-// Each iteration is straight-line code over 4 blocks and 2 register buffers:
-// loads are unconditional (indices past the window are clamped to its last
-// block and their compute is skipped), so the wait before each compute covers
-// exactly the buffer it reads while the other buffer stays in flight.
+// Walk blocks [blk0, blk0 + n_blk) of one (sequence, kv head); keys at
+// positions >= L are masked.  Block ids are fetched once per
+// 64 blocks into a VGPR and read back per block with v_readlane, so no table
+// load sits in the pipeline.  Blocks go in straight-line groups of 4 over 2
+// register buffers (the wait before each compute covers exactly the buffer it
+// reads while the other stays in flight); a window's last 1-3 blocks take a
+// straight-line tail of their own, so no load is ever issued for a block that
+// is not computed.
 __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
                                             const uint16_t* __restrict__ vpool,
                                             const int32_t* __restrict__ trow, int h, int blk0,
-                                            int blk1, int L, const uint32_t (&qv)[kGroup][2][4],
+                                            int n_blk, int L, const uint32_t (&qv)[kGroup][2][4],
                                             float scale_log2, uint16_t* lds_p, WaveState& st,
                                             int wave, int lane) {
     BlockRegs r0, r1;
     constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
 #define KVC_LOAD_WIN(R, I)                                                                          \
     {                                                                                               \
-        const int ii_ = min((I), wn - 1);                                                           \
-        const size_t off_ = ((size_t)__builtin_amdgcn_readlane(my_id, ii_) * kKvHeads + h) * kUnitElems; \
+        const size_t off_ = ((size_t)__builtin_amdgcn_readlane(my_id, (I)) * kKvHeads + h) * kUnitElems; \
         load_block(R, kpool + off_, vpool + off_, wave, lane);                                     \
     }
-    for (int w0 = blk0; w0 < blk1; w0 += 64) {
-        const int wn = min(64, blk1 - w0);
-        const int my_id = lane < wn ? trow[w0 + lane] : 0;
-        for (int i = 0; i < wn; i += 4) {
-            const int nv0 = min(kBlockTok, L - (w0 + i) * kBlockTok);
-            const int nv1 = min(kBlockTok, L - (w0 + i + 1) * kBlockTok);
-            const int nv2 = min(kBlockTok, L - (w0 + i + 2) * kBlockTok);
-            const int nv3 = min(kBlockTok, L - (w0 + i + 3) * kBlockTok);
+#define KVC_NV(I) min(kBlockTok, L - (blk0 + w0 + (I)) * kBlockTok)
+#define KVC_COMPUTE(R, I) compute_block(R, qv, KVC_NV(I), scale_log2, lds_p, st, wave, lane)
+    for (int w0 = 0; w0 < n_blk; w0 += 64) {
+        const int wn = min(64, n_blk - w0);
+        const int my_id = lane < wn ? trow[blk0 + w0 + lane] : 0;
+        int i = 0;
+        for (; i + 4 <= wn; i += 4) {
             KVC_LOAD_WIN(r0, i)
             KVC_LOAD_WIN(r1, i + 1)
-            compute_block(r0, qv, nv0, scale_log2, lds_p, st, wave, lane);
+            KVC_COMPUTE(r0, i);
             KVC_LOAD_WIN(r0, i + 2)
-            if (i + 1 < wn) compute_block(r1, qv, nv1, scale_log2, lds_p, st, wave, lane);
+            KVC_COMPUTE(r1, i + 1);
             KVC_LOAD_WIN(r1, i + 3)
-            if (i + 2 < wn) compute_block(r0, qv, nv2, scale_log2, lds_p, st, wave, lane);
-            if (i + 3 < wn) compute_block(r1, qv, nv3, scale_log2, lds_p, st, wave, lane);
+            KVC_COMPUTE(r0, i + 2);
+            KVC_COMPUTE(r1, i + 3);
+        }
+        const int rem = wn - i;
+        if (rem == 1) {
+            KVC_LOAD_WIN(r0, i)
+            KVC_COMPUTE(r0, i);
+        } else if (rem == 2) {
+            KVC_LOAD_WIN(r0, i)
+            KVC_LOAD_WIN(r1, i + 1)
+            KVC_COMPUTE(r0, i);
+            KVC_COMPUTE(r1, i + 1);
+        } else if (rem == 3) {
+            KVC_LOAD_WIN(r0, i)
+            KVC_LOAD_WIN(r1, i + 1)
+            KVC_COMPUTE(r0, i);
+            KVC_LOAD_WIN(r0, i + 2)
+            KVC_COMPUTE(r1, i + 1);
+            KVC_COMPUTE(r0, i + 2);
         }
     }
+#undef KVC_COMPUTE
+#undef KVC_NV
 #undef KVC_LOAD_WIN
 }
 
@@ -425,9 +438,58 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
 // the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8).  Each item
 // writes (m, l, acc) for its 4 q heads; the last item of a (seq, head) to
 // arrive (device-scope counter) combines them and writes the output.
-constexpr int kCombineBatch = 8;
+constexpr int kCombineBatch = 32;
 
-__global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<kDppXor1>(x));
+    x = fmaxf(x, dpp<kDppXor2>(x));
+    x = fmaxf(x, dpp<kDppHalfMirror>(x));  // quads already uniform: pairs quad 0 with quad 1
+    x = fmaxf(x, dpp<kDppRowRor8>(x));
+    x = max_xor16(x);
+    return max_xor32(x);
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    x += dpp<kDppRowRor8>(x);
+    x = sum_xor16(x);
+    return sum_xor32(x);
+}
+
+// Fold partials [item0, item0 + nk) (nk <= NB) of q head g into (Mc, Lc, Ac).
+// All NB acc loads (indices past nk clamped, weight 0) and the (m, l) load of
+// lane k's partial are issued before any is consumed.
+template <int NB>
+__device__ __forceinline__ void combine_batch(__amdgpu_buffer_rsrc_t prs, int item0, int nk, int g, int d0,
+                                              int lane, float& Mc, float& Lc, float (&Ac)[4]) {
+    const int kl = min(lane, nk - 1);
+    const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(
+        prs, ((item0 + kl) * kItemFloats + kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
+    u32x4 pa[NB];
+#pragma unroll
+    for (int k = 0; k < NB; k++)
+        pa[k] = __builtin_amdgcn_raw_buffer_load_b128(
+            prs, ((item0 + min(k, nk - 1)) * kItemFloats + g * kHeadDim + d0) * 4, 0, kCpolSC1);
+    __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
+    const bool own = lane < nk;
+    const float m_l = own ? __uint_as_float(ml[0]) : kNegBig;
+    const float mb = fmaxf(Mc, wave_max(m_l));
+    const float cc = fast_exp2(Mc - mb);
+    Mc = mb;
+    const float w_l = own ? fast_exp2(m_l - mb) : 0.f;
+    Lc = fmaf(Lc, cc, wave_sum(w_l * __uint_as_float(ml[1])));
+#pragma unroll
+    for (int j = 0; j < 4; j++) Ac[j] *= cc;
+#pragma unroll
+    for (int k = 0; k < NB; k++) {
+        const float w = readlane(w_l, k);
+#pragma unroll
+        for (int j = 0; j < 4; j++) Ac[j] = fmaf(w, __uint_as_float(pa[k][j]), Ac[j]);
+    }
+}
+
+__global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     __shared__ DecodeSmem sm;
     const int b = blockIdx.x;
     const int item = (b & 7) * a.per_xcd + (b >> 3);
@@ -458,7 +520,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     // chunk that owns it, which also writes it into the pool
     const int Lw = a.k_new ? L - 1 : L;
     const int wblk1 = min(blk1, (Lw + kBlockTok - 1) / kBlockTok);
-    walk_blocks(a.kpool, a.vpool, trow, h, blk0, wblk1, Lw, qv, a.scale_log2, sm.p16[wave], st, wave, lane);
+    walk_blocks(a.kpool, a.vpool, trow, h, blk0, max(0, wblk1 - blk0), Lw, qv, a.scale_log2, sm.p16[wave], st,
+                wave, lane);
     finalize_l(st);
     const bool owns_new = new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
     if (owns_new) {
@@ -502,46 +565,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(DecodeArgs a) {
     }
     __syncthreads();
     if (!sm.last) return;
-    // combine the n_chunks partials of (s, h) in batches; the next batch's
-    // loads are issued before the current batch is reduced
-    const int first = (h * a.total_chunks + a.chunk_begin[s]) * kItemFloats * 4;
+    // combine the n_chunks partials of (s, h): wave g takes q head g; every
+    // partial of a batch is requested at once (lane k also fetches partial
+    // k's (m, l)), then the acc rows are folded in arrival order
+    const int first = h * a.total_chunks + a.chunk_begin[s];
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
-    u32x4 pa[2][kCombineBatch];
-    u32x2 pm[2][kCombineBatch];
-    auto fetch = [&](int buf, int k0) {
-#pragma unroll
-        for (int k = 0; k < kCombineBatch; k++) {
-            const int kb = first + min(k0 + k, n_chunks - 1) * kItemFloats * 4;
-            pa[buf][k] = __builtin_amdgcn_raw_buffer_load_b128(prs, kb + (g * kHeadDim + d0) * 4, 0, kCpolSC1);
-            pm[buf][k] = __builtin_amdgcn_raw_buffer_load_b64(prs, kb + (kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
-        }
-    };
-    auto reduce = [&](int buf, int k0) {
-        float mb = Mc;
-#pragma unroll
-        for (int k = 0; k < kCombineBatch; k++)
-            if (k0 + k < n_chunks) mb = fmaxf(mb, __uint_as_float(pm[buf][k][0]));
-        const float cc = fast_exp2(Mc - mb);
-        Lc *= cc;
-        Ac[0] *= cc; Ac[1] *= cc; Ac[2] *= cc; Ac[3] *= cc;
-        Mc = mb;
-#pragma unroll
-        for (int k = 0; k < kCombineBatch; k++) {
-            const float w = (k0 + k < n_chunks) ? fast_exp2(__uint_as_float(pm[buf][k][0]) - Mc) : 0.f;
-            Lc = fmaf(w, __uint_as_float(pm[buf][k][1]), Lc);
-            Ac[0] = fmaf(w, __uint_as_float(pa[buf][k][0]), Ac[0]);
-            Ac[1] = fmaf(w, __uint_as_float(pa[buf][k][1]), Ac[1]);
-            Ac[2] = fmaf(w, __uint_as_float(pa[buf][k][2]), Ac[2]);
-            Ac[3] = fmaf(w, __uint_as_float(pa[buf][k][3]), Ac[3]);
-        }
-    };
-    fetch(0, 0);
-    for (int k0 = 0; k0 < n_chunks; k0 += 2 * kCombineBatch) {
-        if (k0 + kCombineBatch < n_chunks) fetch(1, k0 + kCombineBatch);
-        reduce(0, k0);
-        if (k0 + kCombineBatch >= n_chunks) break;
-        if (k0 + 2 * kCombineBatch < n_chunks) fetch(0, k0 + 2 * kCombineBatch);
-        reduce(1, k0 + kCombineBatch);
+    for (int k0 = 0; k0 < n_chunks; k0 += kCombineBatch) {
+        const int nk = min(kCombineBatch, n_chunks - k0);
+        if (nk <= 8)
+            combine_batch<8>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
+        else if (nk <= 16)
+            combine_batch<16>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
+        else
+            combine_batch<32>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
     }
     write_out(a.out, a.out_bf16, orow, d0, grow, Lc, Ac);
     if (t == 0) a.counters[s * kKvHeads + h] = 0;
@@ -809,43 +845,47 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a, int n_units) 
     *reinterpret_cast<uint4*>(to + dst) = *reinterpret_cast<const uint4*>(from + src);
 }
 
-// Gather: workgroup = (sequence, 32 consecutive output tokens); output rows
-// are [tok][kv_head][d] packed back to back.  Each thread moves 16 x 16 B of K
-// then of V, all loads issued before the stores.
+// Gather: work item = (sequence, 32 consecutive output tokens), split over 8
+// workgroups = (K or V) x (8-token quarter); output rows are [tok][kv_head][d]
+// packed back to back.  A workgroup moves 16 KiB: each thread 4 x 16 B, all
+// loads issued before the stores.  The quarter's at most two block ids are
+// read once per workgroup (scalar loads), so no table load precedes a data
+// load.
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
-    const int item = blockIdx.x;
+    const int item = blockIdx.x >> 3;
+    const int kv = (blockIdx.x >> 2) & 1, q8 = blockIdx.x & 3;
     int s = 0;
     while (s + 1 < a.n_seqs && a.item_begin[s + 1] <= item) s++;
     const int c = item - a.item_begin[s];
     const int n_tok = a.out_begin[s + 1] - a.out_begin[s];
-    const int t0 = c * kBlockTok;
-    const int nt = min(kBlockTok, n_tok - t0);
+    const int t0 = c * kBlockTok + q8 * 8;
+    const int nt = min(8, n_tok - t0);
+    if (nt <= 0) return;
     const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
-    constexpr int kRowUnits = kHeadDim * 2 / 16;           // 32 x 16 B per row
-    constexpr int kUnits = kBlockTok * kKvHeads * kRowUnits;  // 4096 per tensor
-    constexpr int kPer = kUnits / 256;                      // 16 per thread
+    const int p0 = a.tok0 + t0;
+    const int blk_a = p0 / kBlockTok;
+    const int id_a = trow[blk_a], id_b = trow[(p0 + nt - 1) / kBlockTok];
+    const uint16_t* __restrict__ pool = kv ? a.vpool : a.kpool;
+    uint16_t* __restrict__ outp = (kv ? a.v_out : a.k_out) + ((size_t)a.out_begin[s] + t0) * kKvHeads * kHeadDim;
+    constexpr int kRowUnits = kHeadDim * 2 / 16;  // 32 x 16 B per (token, head) row
+    constexpr int kPer = 8 * kKvHeads * kRowUnits / 256;  // 4
+    u32x4 buf[kPer];
 #pragma unroll
-    for (int kv = 0; kv < 2; kv++) {
-        const uint16_t* pool = kv ? a.vpool : a.kpool;
-        uint16_t* outp = (kv ? a.v_out : a.k_out) + ((size_t)a.out_begin[s] + t0) * kKvHeads * kHeadDim;
-        u32x4 buf[kPer];
+    for (int j = 0; j < kPer; j++) {
+        const int u = j * 256 + (int)threadIdx.x;
+        const int tok = u / (kKvHeads * kRowUnits);
+        const int hh = (u / kRowUnits) % kKvHeads;
+        const int part = u % kRowUnits;
+        const int pos = p0 + min(tok, nt - 1);
+        const int id = pos / kBlockTok == blk_a ? id_a : id_b;
+        const size_t src = (((size_t)id * kKvHeads + hh) * kBlockTok + pos % kBlockTok) * kHeadDim + part * 8;
+        buf[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pool + src));
+    }
 #pragma unroll
-        for (int j = 0; j < kPer; j++) {
-            const int u = j * 256 + threadIdx.x;
-            const int tok = u / (kKvHeads * kRowUnits);
-            const int hh = (u / kRowUnits) % kKvHeads;
-            const int part = u % kRowUnits;
-            const int pos = a.tok0 + t0 + min(tok, nt - 1);
-            const size_t src = (((size_t)trow[pos / kBlockTok] * kKvHeads + hh) * kBlockTok + pos % kBlockTok) *
-                                   kHeadDim + part * 8;
-            buf[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pool + src));
-        }
-#pragma unroll
-        for (int j = 0; j < kPer; j++) {
-            const int u = j * 256 + threadIdx.x;
-            if (u / (kKvHeads * kRowUnits) < nt)
-                __builtin_nontemporal_store(buf[j], reinterpret_cast<u32x4*>(outp + (size_t)u * 8));
-        }
+    for (int j = 0; j < kPer; j++) {
+        const int u = j * 256 + (int)threadIdx.x;
+        if (u / (kKvHeads * kRowUnits) < nt)
+            __builtin_nontemporal_store(buf[j], reinterpret_cast<u32x4*>(outp + (size_t)u * 8));
     }
 }
 
@@ -951,7 +991,7 @@ int launch_table_update(const TableUpdateArgs& a, void* stream) {
 
 int launch_decode(const DecodeArgs& a, void* stream) {
     const int grid = a.per_xcd * 8;
-    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
@@ -969,7 +1009,7 @@ int launch_append(const AppendArgs& a, int n_units, void* stream) {
 
 int launch_gather(const GatherArgs& a, void* stream) {
     if (a.n_items <= 0) return 0;
-    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)a.n_items), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)a.n_items * 8), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
