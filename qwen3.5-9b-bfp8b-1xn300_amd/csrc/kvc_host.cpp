@@ -1016,6 +1016,10 @@ int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_s
         a.table_stride = c->max_blocks;
         a.n_seqs = n;
         a.n_q = n_q;
+        a.n_groups = n * kKvHeads;
+        for (int32_t j = 0; j < n; j++) a.seq_order[j] = j;
+        std::stable_sort(a.seq_order, a.seq_order + n,
+                         [&](int32_t x, int32_t y) { return a.q_pos0[x] > a.q_pos0[y]; });
         int e = launch_prefill(a, stream);
         if (e) return hip_err((hipError_t)e, "prefill launch");
     }

@@ -117,8 +117,11 @@ struct PrefillArgs {
     int32_t n_seqs;
     int32_t n_q;
     int32_t pad;
+    int32_t n_groups;           // n_seqs * Hkv (sequence, kv head) groups
+    int32_t pad2;
     int32_t slot[kMaxBatch];
     int32_t q_pos0[kMaxBatch];  // position of query row 0
+    int32_t seq_order[kMaxBatch];  // batch indices, most keys first
 };
 
 // Snapshot copy: per pair, state bytes then the K/V segment.

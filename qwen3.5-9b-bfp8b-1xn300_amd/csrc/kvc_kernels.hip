@@ -597,23 +597,33 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 // leaves the S^T accumulator already in B-operand order.  Keys inside one
 // 32-key MFMA step are taken in the order (4q + i, 16 + 4q + i) for lane group
 // q = lane / 16, i = 0..3, on both operands (a consistent permutation of the
-// summation index).  K and V tiles are staged row-major (token rows, 16-B
-// writes); the V^T operand is read with ds_read_b64_tr_b16, which hands lane
-// i of each 16-lane group element i%4 of the 8-B pieces addressed by lanes
-// i/4, 4 + i/4, 8 + i/4, 12 + i/4 -- a 4 x 16 transpose.  The next tile's
-// global loads are issued before the current tile is computed.
+// summation index).  K and V tiles go straight from global memory into LDS
+// (global_load_lds_dwordx4, no register staging), double buffered: tile t+1
+// is in flight while tile t is computed, one barrier per tile.  Tile rows are
+// 512 B with their 16-B chunks XOR-swizzled by the row (chunk c of row r sits
+// at position c ^ (r % 16)), which keeps both operand reads free of bank
+// conflicts.  The V^T operand is read with ds_read_b64_tr_b16, which hands
+// lane i of each 16-lane group element i%4 of the 8-B pieces addressed by
+// lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4 -- a 4 x 16 transpose.  Rows past the
+// sequence end are loaded from the last valid key (finite data; their weight
+// is 0).
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 constexpr int kPfRows = 32;                 // query positions per workgroup
 constexpr int kPfKeys = 64;                 // keys per tile
-constexpr int kKStride = kHeadDim + 8;      // K / V tile row stride (elements), 528 B
+constexpr int kTileElems = kPfKeys * kHeadDim;
+constexpr int kPfAhead = 4;                 // operand fragments read ahead of their MFMAs
 
 struct PrefillSmem {
-    uint16_t k[kPfKeys * kKStride];
-    uint16_t v[kPfKeys * kKStride];
+    uint16_t kv[2][2][kTileElems];  // [buffer][K | V][row * 256 + swizzled column]
 };
 
+// element offset of (row r, element e) in a swizzled tile
+__device__ __forceinline__ int swz(int r, int e) { return r * kHeadDim + ((((e >> 3) ^ (r & 15))) << 3) + (e & 7); }
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
     const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -624,11 +634,20 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void prefill_mfma_kernel(PrefillArgs a) {
     __shared__ PrefillSmem sm;
+    // Workgroup b runs on XCD b % 8.  The n_pb query blocks of one (sequence,
+    // kv head) group share its K/V, so they go to one XCD (one L2), in
+    // consecutive dispatch rounds; groups are taken most keys first (the
+    // sequence order is sorted on the host) and, inside a group, the later
+    // (longer) query blocks first.
     const int n_pb = (a.n_q + kPfRows - 1) / kPfRows;
-    const int pb = blockIdx.x % n_pb;
-    const int h = (blockIdx.x / n_pb) % kKvHeads;
-    const int s = blockIdx.x / (n_pb * kKvHeads);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int xcd = blockIdx.x & 7, round = blockIdx.x >> 3;
+    const int grp = (round / n_pb) * 8 + xcd;
+    if (grp >= a.n_groups) return;
+    const int pb = n_pb - 1 - round % n_pb;
+    const int h = grp % kKvHeads;
+    const int s = a.seq_order[grp / kKvHeads];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS DMA base)
     const int q4 = lane >> 4, r16 = lane & 15;
     const int g = wave;
     const int pos0 = a.q_pos0[s];
@@ -655,20 +674,22 @@ void prefill_mfma_kernel(PrefillArgs a) {
     // and are read with v_readlane: no dependent table load on the fetch path
     int idw0 = 0;
     int idv = lane < n_blocks ? trow[lane] : 0;
-    // global -> register staging of one tile: thread owns 16-B pieces
-    // u = j*256 + tid (j = 0..7) of the 64 x 256 K and V token rows
-    u32x4 kst[8], vst[8];
-    auto fetch_tile = [&](int t) {
-        const int b0 = min(2 * t, n_blocks - 1), b1 = min(2 * t + 1, n_blocks - 1);
-        const size_t u0 = ((size_t)__builtin_amdgcn_readlane(idv, b0 - idw0) * kKvHeads + h) * kUnitElems;
-        const size_t u1 = ((size_t)__builtin_amdgcn_readlane(idv, b1 - idw0) * kKvHeads + h) * kUnitElems;
+    // wave w loads tile rows 16w .. 16w+15, two per instruction (lanes 0-31:
+    // row 16w + 2j, lanes 32-63: the next row); lane l fills chunk position
+    // l % 32 of its row, i.e. global chunk (l % 32) ^ (row % 16)
+    auto issue_tile = [&](int t, int buf) {
+        const int last = kmax - 1 - t * kPfKeys;  // last valid row of the tile
+        const int ida = __builtin_amdgcn_readlane(idv, 2 * t - idw0);
+        const int idb = __builtin_amdgcn_readlane(idv, min(2 * t + 1, n_blocks - 1) - idw0);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int u = j * 256 + tid;
-            const int key = u >> 5;  // 0..63 within the tile; j < 4 -> first block
-            const size_t off = (j < 4 ? u0 : u1) + (key % kBlockTok) * kHeadDim + (u & 31) * 8;
-            kst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.kpool + off));
-            vst[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(a.vpool + off));
+            const int r0 = 16 * wave + 2 * j;
+            const int r = r0 + (lane >> 5);
+            const int rs = min(r, last);
+            const size_t src = ((size_t)(rs < kBlockTok ? ida : idb) * kKvHeads + h) * kUnitElems +
+                               (rs & (kBlockTok - 1)) * kHeadDim + (((lane & 31) ^ (r & 15)) << 3);
+            __builtin_amdgcn_global_load_lds(a.kpool + src, (lds_ptr_t)&sm.kv[buf][0][r0 * kHeadDim], 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.vpool + src, (lds_ptr_t)&sm.kv[buf][1][r0 * kHeadDim], 16, 0, 0);
         }
     };
 
@@ -678,58 +699,71 @@ void prefill_mfma_kernel(PrefillArgs a) {
     float m_run[2] = {kNegBig, kNegBig};
     float l_lane[2] = {0.f, 0.f};
 
-    fetch_tile(0);
+    issue_tile(0, 0);
     for (int t = 0; t < n_tiles; t++) {
-        __syncthreads();  // previous tile's LDS reads are done
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int u = j * 256 + tid;
-            const int key = u >> 5, col = (u & 31) * 8;
-            // keys past the sequence end come from stale slots: zero them so
-            // no NaN bit pattern reaches the MFMA (their p is 0 already)
-            const bool live = t * kPfKeys + key < kmax;
-            const u32x4 z = {0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x4*>(&sm.k[key * kKStride + col]) = live ? kst[j] : z;
-            *reinterpret_cast<u32x4*>(&sm.v[key * kKStride + col]) = live ? vst[j] : z;
-        }
+        // own loads of tile t have landed; after the barrier every wave's
+        // have, and every wave is done reading buffer (t+1)&1 (tile t-1)
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (t + 1 < n_tiles) {
             if (2 * (t + 1) + 1 - idw0 >= 64 && 2 * (t + 1) < n_blocks) {  // uniform: next id window
                 idw0 = 2 * (t + 1);
                 idv = idw0 + lane < n_blocks ? trow[idw0 + lane] : 0;
             }
-            fetch_tile(t + 1);
+            issue_tile(t + 1, (t + 1) & 1);
         }
+        const uint16_t* ks_ = sm.kv[t & 1][0];
+        const uint16_t* vs_ = sm.kv[t & 1][1];
 
-        // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16
+        // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16.
+        // The 32 K fragments (kt, ks) are read kPfAhead steps ahead of their
+        // MFMAs through a small register ring.
         f32x4 st[4][2];
+        bf16x8_t kf[kPfAhead];
+        auto read_kfrag = [&](int i) {
+            const int kt = i >> 3, ks = i & 7;
+            kf[i % kPfAhead] = as_bf16x8(*reinterpret_cast<const u32x4*>(&ks_[swz(16 * kt + r16, 32 * ks + 8 * q4)]));
+        };
 #pragma unroll
-        for (int kt = 0; kt < 4; kt++) {
-            st[kt][0] = st[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < kPfAhead; i++) read_kfrag(i);
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                const bf16x8_t ka = as_bf16x8(
-                    *reinterpret_cast<const u32x4*>(&sm.k[(16 * kt + r16) * kKStride + 32 * ks + 8 * q4]));
-                st[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[0][ks], st[kt][0], 0, 0, 0);
-                st[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[1][ks], st[kt][1], 0, 0, 0);
-            }
+        for (int i = 0; i < 32; i++) {
+            const int kt = i >> 3, ks = i & 7;
+            if (ks == 0) st[kt][0] = st[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const bf16x8_t ka = kf[i % kPfAhead];
+            if (i + kPfAhead < 32) read_kfrag(i + kPfAhead);
+            st[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[0][ks], st[kt][0], 0, 0, 0);
+            st[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[1][ks], st[kt][1], 0, 0, 0);
         }
-        // scale, causal mask, online softmax (lazy rescale with slack)
+        // scale, causal mask (only on tiles that reach the diagonal or the
+        // sequence end), online softmax (lazy rescale with slack)
+        const bool full_tile = t * kPfKeys + kPfKeys - 1 <= pos0 + row0 && t * kPfKeys + kPfKeys <= kmax;
         bool need = false;
         float mt[2];
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
             const int qpos = pos0 + row0 + 16 * nt + r16;
             float mx = kNegBig;
+            if (full_tile) {
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++)
+                for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int kp = t * kPfKeys + 16 * kt + 4 * q4 + i;
-                    const float v = (kp <= qpos && kp < kmax) ? st[kt][nt][i] * a.scale_log2 : kNegBig;
-                    st[kt][nt][i] = v;
-                    mx = fmaxf(mx, v);
-                }
+                    for (int i = 0; i < 4; i++) {
+                        const float v = st[kt][nt][i] * a.scale_log2;
+                        st[kt][nt][i] = v;
+                        mx = fmaxf(mx, v);
+                    }
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int kp = t * kPfKeys + 16 * kt + 4 * q4 + i;
+                        const float v = (kp <= qpos && kp < kmax) ? st[kt][nt][i] * a.scale_log2 : kNegBig;
+                        st[kt][nt][i] = v;
+                        mx = fmaxf(mx, v);
+                    }
+            }
             mx = max_xor16(mx);
             mx = max_xor32(mx);
             mt[nt] = mx;
@@ -770,22 +804,29 @@ void prefill_mfma_kernel(PrefillArgs a) {
         // O^T += V^T . P^T; the V^T operand of lane (q4, r16) is V[keys
         // 32kk + 4q4 + e (+16)][16dt + r16]: lane J of the group addresses
         // row 32kk + 4q4 + J/4 (+16), dims 16dt + 4(J%4) .. +3
+        // V^T fragments (dt, kk), read kPfAhead steps ahead of their MFMAs
+        bf16x8_t vf[kPfAhead];
+        auto read_vfrag = [&](int i) {
+            const int dt = i >> 1, kk = i & 1;
+            const int vr = 32 * kk + 4 * q4 + (r16 >> 2);
+            const u32x2 lo = lds_read_tr16(&vs_[swz(vr, 16 * dt + 4 * (r16 & 3))]);
+            const u32x2 hi = lds_read_tr16(&vs_[swz(vr + 16, 16 * dt + 4 * (r16 & 3))]);
+            u32x4 w;
+            w[0] = lo[0];
+            w[1] = lo[1];
+            w[2] = hi[0];
+            w[3] = hi[1];
+            vf[i % kPfAhead] = as_bf16x8(w);
+        };
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++) {
+        for (int i = 0; i < kPfAhead; i++) read_vfrag(i);
 #pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                const uint16_t* vp = &sm.v[(32 * kk + 4 * q4 + (r16 >> 2)) * kKStride + 16 * dt + 4 * (r16 & 3)];
-                const u32x2 lo = lds_read_tr16(vp);
-                const u32x2 hi = lds_read_tr16(vp + 16 * kKStride);
-                u32x4 w;
-                w[0] = lo[0];
-                w[1] = lo[1];
-                w[2] = hi[0];
-                w[3] = hi[1];
-                const bf16x8_t va = as_bf16x8(w);
-                o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[0][kk], o[dt][0], 0, 0, 0);
-                o[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[1][kk], o[dt][1], 0, 0, 0);
-            }
+        for (int i = 0; i < 32; i++) {
+            const int dt = i >> 1, kk = i & 1;
+            const bf16x8_t va = vf[i % kPfAhead];
+            if (i + kPfAhead < 32) read_vfrag(i + kPfAhead);
+            o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[0][kk], o[dt][0], 0, 0, 0);
+            o[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[1][kk], o[dt][1], 0, 0, 0);
         }
     }
     // epilogue: row sums across the 4 lane groups, normalise, gate, store
@@ -996,7 +1037,7 @@ int launch_decode(const DecodeArgs& a, void* stream) {
 }
 
 int launch_prefill(const PrefillArgs& a, void* stream) {
-    const int grid = a.n_seqs * kKvHeads * ((a.n_q + kPfRows - 1) / kPfRows);
+    const int grid = 8 * ((a.n_groups + 7) / 8) * ((a.n_q + kPfRows - 1) / kPfRows);
     hipLaunchKernelGGL(prefill_mfma_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
