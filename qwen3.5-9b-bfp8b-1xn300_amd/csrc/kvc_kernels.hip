@@ -613,6 +613,10 @@ constexpr int kPfRows = 32;                 // query positions per workgroup
 constexpr int kPfKeys = 64;                 // keys per tile
 constexpr int kTileElems = kPfKeys * kHeadDim;
 constexpr int kPfAhead = 4;                 // operand fragments read ahead of their MFMAs
+#ifndef KVC_PF_NT
+#define KVC_PF_NT 1
+#endif
+constexpr int kPfNT = KVC_PF_NT;            // 16-row query tiles per prefill wave (1 or 2)
 
 struct PrefillSmem {
     uint16_t kv[2][2][kTileElems];  // [buffer][K | V][row * 256 + swizzled column]
@@ -631,8 +635,15 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(u32x2, r);
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// NT = 16-row query tiles per wave: NT = 2 runs 4 waves (one per q head of
+// the group, 32 rows each); NT = 1 runs 8 waves (q head, row half), two per
+// SIMD, so one wave's MFMAs overlap the other's LDS reads and softmax.
+template <int NT>
+__global__ __launch_bounds__(64 * 8 / NT) __attribute__((amdgpu_waves_per_eu(2 / NT, 2 / NT)))
 void prefill_mfma_kernel(PrefillArgs a) {
+    constexpr int kWavesPf = 8 / NT;
+    constexpr int kRowsPerWave = 16 * NT;
+    constexpr int kLoadRows = kPfKeys / kWavesPf;  // tile rows each wave loads
     __shared__ PrefillSmem sm;
     // Workgroup b runs on XCD b % 8.  The n_pb query blocks of one (sequence,
     // kv head) group share its K/V, so they go to one XCD (one L2), in
@@ -649,7 +660,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (LDS DMA base)
     const int q4 = lane >> 4, r16 = lane & 15;
-    const int g = wave;
+    const int g = wave & 3;            // q head of the group
+    const int rw0 = (wave >> 2) * kRowsPerWave;  // first row of the wave within the tile
     const int pos0 = a.q_pos0[s];
     const int row0 = pb * kPfRows;                     // first query row of the tile
     const int rows = min(kPfRows, a.n_q - row0);
@@ -659,11 +671,11 @@ void prefill_mfma_kernel(PrefillArgs a) {
     const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
     constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
 
-    // Q^T as the B operand: qb[nt][ks] = q[row 16nt + r16][d 32ks + 8q4 .. +7]
-    bf16x8_t qb[2][8];
+    // Q^T as the B operand: qb[nt][ks] = q[row rw0 + 16nt + r16][d 32ks + 8q4 .. +7]
+    bf16x8_t qb[NT][8];
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const int r = row0 + min(16 * nt + r16, rows - 1);
+    for (int nt = 0; nt < NT; nt++) {
+        const int r = row0 + min(rw0 + 16 * nt + r16, rows - 1);
         const uint16_t* qr = a.q + (((size_t)s * a.n_q + r) * kQHeads + h * kGroup + g) * kHeadDim;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
@@ -674,16 +686,16 @@ void prefill_mfma_kernel(PrefillArgs a) {
     // and are read with v_readlane: no dependent table load on the fetch path
     int idw0 = 0;
     int idv = lane < n_blocks ? trow[lane] : 0;
-    // wave w loads tile rows 16w .. 16w+15, two per instruction (lanes 0-31:
-    // row 16w + 2j, lanes 32-63: the next row); lane l fills chunk position
-    // l % 32 of its row, i.e. global chunk (l % 32) ^ (row % 16)
+    // wave w loads tile rows kLoadRows*w .., two per instruction (lanes 0-31:
+    // row r0, lanes 32-63: the next row); lane l fills chunk position l % 32
+    // of its row, i.e. global chunk (l % 32) ^ (row % 16)
     auto issue_tile = [&](int t, int buf) {
         const int last = kmax - 1 - t * kPfKeys;  // last valid row of the tile
         const int ida = __builtin_amdgcn_readlane(idv, 2 * t - idw0);
         const int idb = __builtin_amdgcn_readlane(idv, min(2 * t + 1, n_blocks - 1) - idw0);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int r0 = 16 * wave + 2 * j;
+        for (int j = 0; j < kLoadRows / 2; j++) {
+            const int r0 = kLoadRows * wave + 2 * j;
             const int r = r0 + (lane >> 5);
             const int rs = min(r, last);
             const size_t src = ((size_t)(rs < kBlockTok ? ida : idb) * kKvHeads + h) * kUnitElems +
@@ -693,11 +705,19 @@ void prefill_mfma_kernel(PrefillArgs a) {
         }
     };
 
-    f32x4 o[16][2];
+    // With NT = 2 the accumulators outgrow the VGPRs: an (empty) statement
+    // with an AGPR operand makes the compiler select the AGPR-accumulator form
+    // of the MFMAs, so O^T lives in AGPRs.
+    if constexpr (NT == 2) asm volatile("" ::"a"(0));
+    f32x4 o[16][NT];
+    float m_run[NT], l_lane[NT];
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++) o[dt][0] = o[dt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float m_run[2] = {kNegBig, kNegBig};
-    float l_lane[2] = {0.f, 0.f};
+    for (int nt = 0; nt < NT; nt++) {
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        m_run[nt] = kNegBig;
+        l_lane[nt] = 0.f;
+    }
 
     issue_tile(0, 0);
     for (int t = 0; t < n_tiles; t++) {
@@ -718,7 +738,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
         // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16.
         // The 32 K fragments (kt, ks) are read kPfAhead steps ahead of their
         // MFMAs through a small register ring.
-        f32x4 st[4][2];
+        f32x4 st[4][NT];
         bf16x8_t kf[kPfAhead];
         auto read_kfrag = [&](int i) {
             const int kt = i >> 3, ks = i & 7;
@@ -729,20 +749,20 @@ void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const int kt = i >> 3, ks = i & 7;
-            if (ks == 0) st[kt][0] = st[kt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
             const bf16x8_t ka = kf[i % kPfAhead];
             if (i + kPfAhead < 32) read_kfrag(i + kPfAhead);
-            st[kt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[0][ks], st[kt][0], 0, 0, 0);
-            st[kt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[1][ks], st[kt][1], 0, 0, 0);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                st[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[kt][nt], 0, 0, 0);
         }
         // scale, causal mask (only on tiles that reach the diagonal or the
         // sequence end), online softmax (lazy rescale with slack)
-        const bool full_tile = t * kPfKeys + kPfKeys - 1 <= pos0 + row0 && t * kPfKeys + kPfKeys <= kmax;
+        const bool full_tile = t * kPfKeys + kPfKeys - 1 <= pos0 + row0 + rw0 && t * kPfKeys + kPfKeys <= kmax;
         bool need = false;
-        float mt[2];
+        float mt[NT];
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const int qpos = pos0 + row0 + 16 * nt + r16;
+        for (int nt = 0; nt < NT; nt++) {
+            const int qpos = pos0 + row0 + rw0 + 16 * nt + r16;
             float mx = kNegBig;
             if (full_tile) {
 #pragma unroll
@@ -769,22 +789,25 @@ void prefill_mfma_kernel(PrefillArgs a) {
             mt[nt] = mx;
             need |= mx > m_run[nt] + kRescaleSlack;
         }
-        if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        if (__builtin_amdgcn_ballot_w64(need) != 0) {  // uniform; rows that keep their max scale by 1
 #pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                if (mt[nt] > m_run[nt] + kRescaleSlack) {
-                    const float c = fast_exp2(m_run[nt] - mt[nt]);
-                    m_run[nt] = mt[nt];
-                    l_lane[nt] *= c;
+            for (int nt = 0; nt < NT; nt++) {
+                const bool up = mt[nt] > m_run[nt] + kRescaleSlack;
+                const float c = up ? fast_exp2(m_run[nt] - mt[nt]) : 1.f;
+                m_run[nt] = up ? mt[nt] : m_run[nt];
+                l_lane[nt] *= c;
+                // the scaled values re-enter the accumulators through an MFMA
+                // with zero operands, which keeps O^T in the MFMA register class
+                const bf16x8_t z8 = {};
 #pragma unroll
-                    for (int dt = 0; dt < 16; dt++) o[dt][nt] *= c;
-                }
+                for (int dt = 0; dt < 16; dt++)
+                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(z8, z8, o[dt][nt] * c, 0, 0, 0);
             }
         }
         // P^T as the B operand (bf16), k-slot order (4q4 + i, 16 + 4q4 + i)
-        bf16x8_t pb_[2][2];
+        bf16x8_t pb_[NT][2];
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
+        for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
             for (int kk = 0; kk < 2; kk++) {
                 u32x4 w;
@@ -825,17 +848,18 @@ void prefill_mfma_kernel(PrefillArgs a) {
             const int dt = i >> 1, kk = i & 1;
             const bf16x8_t va = vf[i % kPfAhead];
             if (i + kPfAhead < 32) read_vfrag(i + kPfAhead);
-            o[dt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[0][kk], o[dt][0], 0, 0, 0);
-            o[dt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[1][kk], o[dt][1], 0, 0, 0);
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[nt][kk], o[dt][nt], 0, 0, 0);
         }
     }
     // epilogue: row sums across the 4 lane groups, normalise, gate, store
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
+    for (int nt = 0; nt < NT; nt++) {
         float l = l_lane[nt];
         l = sum_xor16(l);
         l = sum_xor32(l);
-        const int rl = 16 * nt + r16;
+        const int rl = rw0 + 16 * nt + r16;
         if (rl >= rows) continue;
         const size_t orow = (((size_t)s * a.n_q + row0 + rl) * kQHeads + h * kGroup + g) * kHeadDim;
         const float inv = __builtin_amdgcn_rcpf(l);
@@ -1038,7 +1062,7 @@ int launch_decode(const DecodeArgs& a, void* stream) {
 
 int launch_prefill(const PrefillArgs& a, void* stream) {
     const int grid = 8 * ((a.n_groups + 7) / 8) * ((a.n_q + kPfRows - 1) / kPfRows);
-    hipLaunchKernelGGL(prefill_mfma_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(prefill_mfma_kernel<kPfNT>, dim3(grid), dim3(64 * 8 / kPfNT), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
