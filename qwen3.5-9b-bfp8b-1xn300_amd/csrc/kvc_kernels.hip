@@ -600,9 +600,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 // summation index).  K and V tiles go straight from global memory into LDS
 // (global_load_lds_dwordx4, no register staging), double buffered: tile t+1
 // is in flight while tile t is computed, one barrier per tile.  Tile rows are
-// 512 B with their 16-B chunks XOR-swizzled by the row (chunk c of row r sits
-// at position c ^ (r % 16)), which keeps both operand reads free of bank
-// conflicts.  The V^T operand is read with ds_read_b64_tr_b16, which hands
+// 512 B with their 16-B chunks XOR-swizzled by the row, with one pattern for
+// K and another for V (swz_k, swz_v), so that both operand reads are free of
+// bank conflicts.  The V^T operand is read with ds_read_b64_tr_b16, which hands
 // lane i of each 16-lane group element i%4 of the 8-B pieces addressed by
 // lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4 -- a 4 x 16 transpose.  Rows past the
 // sequence end are loaded from the last valid key (finite data; their weight
@@ -613,6 +613,8 @@ constexpr int kPfRows = 32;                 // query positions per workgroup
 constexpr int kPfKeys = 64;                 // keys per tile
 constexpr int kTileElems = kPfKeys * kHeadDim;
 constexpr int kPfAhead = 4;                 // operand fragments read ahead of their MFMAs
+constexpr int kSgMfma = 0x008;              // sched_group_barrier masks: MFMA,
+constexpr int kSgDsRead = 0x100;            //   LDS read
 #ifndef KVC_PF_NT
 #define KVC_PF_NT 1
 #endif
@@ -622,12 +624,33 @@ struct PrefillSmem {
     uint16_t kv[2][2][kTileElems];  // [buffer][K | V][row * 256 + swizzled column]
 };
 
-// element offset of (row r, element e) in a swizzled tile
-__device__ __forceinline__ int swz(int r, int e) { return r * kHeadDim + ((((e >> 3) ^ (r & 15))) << 3) + (e & 7); }
+// Element offset of (row r, element e) in a swizzled tile: 16-B chunk c of row
+// r sits at position c ^ kswz(r) (K) or c ^ vswz(r) (V).  A K fragment read
+// takes one chunk of 16 rows r16 = 0..15: their positions differ in the low 4
+// bits.  A V^T read (ds_read_b64_tr_b16) takes, per 16-lane group, one chunk
+// pair of 4 rows 4i .. 4i+3: vswz puts the 4 rows on 4 different pairs.
+__device__ __forceinline__ int kswz(int r) { return r & 15; }
+__device__ __forceinline__ int vswz(int r) { return (r & 15) << 1; }
+__device__ __forceinline__ int swz_k(int r, int e) { return r * kHeadDim + (((e >> 3) ^ kswz(r)) << 3) + (e & 7); }
+__device__ __forceinline__ int swz_v(int r, int e) { return r * kHeadDim + (((e >> 3) ^ vswz(r)) << 3) + (e & 7); }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 B per lane from global memory straight into LDS (global_load_lds_dwordx4;
+// lane i writes LDS bytes [lds_off + 16i, +16)).  Issued from inline asm so
+// the compiler does not treat the in-flight copy as a pending write to every
+// LDS object (it would otherwise wait for it before the current tile's
+// reads); callers order it with an explicit s_waitcnt vmcnt(0) and barrier.
+// M0 is set here and used by nothing else in the prefill kernel.
+__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_off) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_off), "v"(gptr)
+                 : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(lds_ptr_t)(p);
+}
 
 __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
     const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -698,10 +721,10 @@ void prefill_mfma_kernel(PrefillArgs a) {
             const int r0 = kLoadRows * wave + 2 * j;
             const int r = r0 + (lane >> 5);
             const int rs = min(r, last);
-            const size_t src = ((size_t)(rs < kBlockTok ? ida : idb) * kKvHeads + h) * kUnitElems +
-                               (rs & (kBlockTok - 1)) * kHeadDim + (((lane & 31) ^ (r & 15)) << 3);
-            __builtin_amdgcn_global_load_lds(a.kpool + src, (lds_ptr_t)&sm.kv[buf][0][r0 * kHeadDim], 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(a.vpool + src, (lds_ptr_t)&sm.kv[buf][1][r0 * kHeadDim], 16, 0, 0);
+            const size_t row = ((size_t)(rs < kBlockTok ? ida : idb) * kKvHeads + h) * kUnitElems +
+                               (rs & (kBlockTok - 1)) * kHeadDim;
+            lds_dma16(a.kpool + row + (((lane & 31) ^ kswz(r)) << 3), lds_addr(&sm.kv[buf][0][r0 * kHeadDim]));
+            lds_dma16(a.vpool + row + (((lane & 31) ^ vswz(r)) << 3), lds_addr(&sm.kv[buf][1][r0 * kHeadDim]));
         }
     };
 
@@ -736,24 +759,32 @@ void prefill_mfma_kernel(PrefillArgs a) {
         const uint16_t* vs_ = sm.kv[t & 1][1];
 
         // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16.
-        // The 32 K fragments (kt, ks) are read kPfAhead steps ahead of their
-        // MFMAs through a small register ring.
+        // Steps i = (ks, kt) run d-slice outer, key subtile inner, so
+        // consecutive MFMAs feed different accumulators; the 32 K fragments
+        // are read kPfAhead steps ahead of their MFMAs through a register ring.
         f32x4 st[4][NT];
         bf16x8_t kf[kPfAhead];
         auto read_kfrag = [&](int i) {
-            const int kt = i >> 3, ks = i & 7;
-            kf[i % kPfAhead] = as_bf16x8(*reinterpret_cast<const u32x4*>(&ks_[swz(16 * kt + r16, 32 * ks + 8 * q4)]));
+            const int ks = i >> 2, kt = i & 3;
+            kf[i % kPfAhead] = as_bf16x8(*reinterpret_cast<const u32x4*>(&ks_[swz_k(16 * kt + r16, 32 * ks + 8 * q4)]));
         };
 #pragma unroll
         for (int i = 0; i < kPfAhead; i++) read_kfrag(i);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
-            const int kt = i >> 3, ks = i & 7;
+            const int ks = i >> 2, kt = i & 3;
             const bf16x8_t ka = kf[i % kPfAhead];
             if (i + kPfAhead < 32) read_kfrag(i + kPfAhead);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
                 st[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[kt][nt], 0, 0, 0);
+        }
+        // pin the pipeline: kPfAhead reads, then (1 read, NT MFMAs) per step
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, kPfAhead, 0);
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            if (i + kPfAhead < 32) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, NT, 0);
         }
         // scale, causal mask (only on tiles that reach the diagonal or the
         // sequence end), online softmax (lazy rescale with slack)
@@ -829,11 +860,11 @@ void prefill_mfma_kernel(PrefillArgs a) {
         // row 32kk + 4q4 + J/4 (+16), dims 16dt + 4(J%4) .. +3
         // V^T fragments (dt, kk), read kPfAhead steps ahead of their MFMAs
         bf16x8_t vf[kPfAhead];
-        auto read_vfrag = [&](int i) {
-            const int dt = i >> 1, kk = i & 1;
+        auto read_vfrag = [&](int i) {  // step i = (kk, dt): consecutive MFMAs feed different o[dt]
+            const int kk = i >> 4, dt = i & 15;
             const int vr = 32 * kk + 4 * q4 + (r16 >> 2);
-            const u32x2 lo = lds_read_tr16(&vs_[swz(vr, 16 * dt + 4 * (r16 & 3))]);
-            const u32x2 hi = lds_read_tr16(&vs_[swz(vr + 16, 16 * dt + 4 * (r16 & 3))]);
+            const u32x2 lo = lds_read_tr16(&vs_[swz_v(vr, 16 * dt + 4 * (r16 & 3))]);
+            const u32x2 hi = lds_read_tr16(&vs_[swz_v(vr + 16, 16 * dt + 4 * (r16 & 3))]);
             u32x4 w;
             w[0] = lo[0];
             w[1] = lo[1];
@@ -845,12 +876,18 @@ void prefill_mfma_kernel(PrefillArgs a) {
         for (int i = 0; i < kPfAhead; i++) read_vfrag(i);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
-            const int dt = i >> 1, kk = i & 1;
+            const int kk = i >> 4, dt = i & 15;
             const bf16x8_t va = vf[i % kPfAhead];
             if (i + kPfAhead < 32) read_vfrag(i + kPfAhead);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
                 o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[nt][kk], o[dt][nt], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2 * kPfAhead, 1);
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            if (i + kPfAhead < 32) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 1);
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, NT, 1);
         }
     }
     // epilogue: row sums across the 4 lane groups, normalise, gate, store
