@@ -612,7 +612,10 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 constexpr int kPfRows = 32;                 // query positions per workgroup
 constexpr int kPfKeys = 64;                 // keys per tile
 constexpr int kTileElems = kPfKeys * kHeadDim;
-constexpr int kPfAhead = 4;                 // operand fragments read ahead of their MFMAs
+#ifndef KVC_PF_AHEAD
+#define KVC_PF_AHEAD 4
+#endif
+constexpr int kPfAhead = KVC_PF_AHEAD;      // operand fragments read ahead of their MFMAs
 constexpr int kSgMfma = 0x008;              // sched_group_barrier masks: MFMA,
 constexpr int kSgDsRead = 0x100;            //   LDS read
 #ifndef KVC_PF_NT
@@ -624,15 +627,13 @@ struct PrefillSmem {
     uint16_t kv[2][2][kTileElems];  // [buffer][K | V][row * 256 + swizzled column]
 };
 
-// Element offset of (row r, element e) in a swizzled tile: 16-B chunk c of row
-// r sits at position c ^ kswz(r) (K) or c ^ vswz(r) (V).  A K fragment read
+// Tile swizzles: 16-B chunk c of row r sits at position c ^ kswz(r) (K) or
+// c ^ vswz(r) (V).  A K fragment read
 // takes one chunk of 16 rows r16 = 0..15: their positions differ in the low 4
 // bits.  A V^T read (ds_read_b64_tr_b16) takes, per 16-lane group, one chunk
 // pair of 4 rows 4i .. 4i+3: vswz puts the 4 rows on 4 different pairs.
 __device__ __forceinline__ int kswz(int r) { return r & 15; }
 __device__ __forceinline__ int vswz(int r) { return (r & 15) << 1; }
-__device__ __forceinline__ int swz_k(int r, int e) { return r * kHeadDim + (((e >> 3) ^ kswz(r)) << 3) + (e & 7); }
-__device__ __forceinline__ int swz_v(int r, int e) { return r * kHeadDim + (((e >> 3) ^ vswz(r)) << 3) + (e & 7); }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
@@ -651,12 +652,17 @@ __device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_off) {
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(lds_ptr_t)(p);
 }
-
-__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+// LDS reads at byte address base + off; off is a compile-time constant that
+// folds into the instruction's offset field.
+__device__ __forceinline__ u32x4 lds_load16(uint32_t base, uint32_t off) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)(base + off));
+}
+__device__ __forceinline__ u32x2 lds_load_tr16(uint32_t base, uint32_t off) {
     const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (i16x4_t __attribute__((address_space(3)))*)(p));
+        (i16x4_t __attribute__((address_space(3)))*)((uintptr_t)(base + off)));
     return __builtin_bit_cast(u32x2, r);
 }
+
 
 // NT = 16-row query tiles per wave: NT = 2 runs 4 waves (one per q head of
 // the group, 32 rows each); NT = 1 runs 8 waves (q head, row half), two per
@@ -742,6 +748,21 @@ void prefill_mfma_kernel(PrefillArgs a) {
         l_lane[nt] = 0.f;
     }
 
+    // Per-lane byte offsets of the operand fragments inside a tile (the XOR
+    // swizzles make them lane dependent, the rest are immediates):
+    //   K (kt, ks = 4hi + j): koff[j] + 256 hi + 8192 kt
+    //   V^T (dt, kk, lo/hi):  voff[dt] + 16384 kk + 8192 (hi)
+    uint32_t koff[4], voff[16];
+#pragma unroll
+    for (int j = 0; j < 4; j++) koff[j] = r16 * 512 + 16 * ((4 * j + q4) ^ r16);
+    {
+        const int w = 4 * q4 + (r16 >> 2);  // V row % 16 of this lane
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+            voff[dt] = w * 512 + 16 * (2 * (dt ^ w) + ((r16 & 3) >> 1)) + 8 * (r16 & 1);
+    }
+    const uint32_t lds_base = lds_addr(&sm.kv[0][0][0]);
+
     issue_tile(0, 0);
     for (int t = 0; t < n_tiles; t++) {
         // own loads of tile t have landed; after the barrier every wave's
@@ -755,8 +776,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
             }
             issue_tile(t + 1, (t + 1) & 1);
         }
-        const uint16_t* ks_ = sm.kv[t & 1][0];
-        const uint16_t* vs_ = sm.kv[t & 1][1];
+        const uint32_t kbuf = lds_base + (t & 1) * (uint32_t)sizeof(sm.kv[0]);  // K tile of this buffer
+        const uint32_t vbuf = kbuf + (uint32_t)sizeof(sm.kv[0][0]);            // V tile
 
         // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16.
         // Steps i = (ks, kt) run d-slice outer, key subtile inner, so
@@ -766,7 +787,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
         bf16x8_t kf[kPfAhead];
         auto read_kfrag = [&](int i) {
             const int ks = i >> 2, kt = i & 3;
-            kf[i % kPfAhead] = as_bf16x8(*reinterpret_cast<const u32x4*>(&ks_[swz_k(16 * kt + r16, 32 * ks + 8 * q4)]));
+            kf[i % kPfAhead] = as_bf16x8(lds_load16(kbuf + koff[ks & 3], 256 * (ks >> 2) + 8192 * kt));
         };
 #pragma unroll
         for (int i = 0; i < kPfAhead; i++) read_kfrag(i);
@@ -862,9 +883,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
         bf16x8_t vf[kPfAhead];
         auto read_vfrag = [&](int i) {  // step i = (kk, dt): consecutive MFMAs feed different o[dt]
             const int kk = i >> 4, dt = i & 15;
-            const int vr = 32 * kk + 4 * q4 + (r16 >> 2);
-            const u32x2 lo = lds_read_tr16(&vs_[swz_v(vr, 16 * dt + 4 * (r16 & 3))]);
-            const u32x2 hi = lds_read_tr16(&vs_[swz_v(vr + 16, 16 * dt + 4 * (r16 & 3))]);
+            const u32x2 lo = lds_load_tr16(vbuf + voff[dt], 16384 * kk);
+            const u32x2 hi = lds_load_tr16(vbuf + voff[dt], 16384 * kk + 8192);
             u32x4 w;
             w[0] = lo[0];
             w[1] = lo[1];
