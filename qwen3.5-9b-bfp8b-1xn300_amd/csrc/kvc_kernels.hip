@@ -1013,8 +1013,9 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
 
 // Snapshot save/restore: per pair, the sequence's whole recurrent state then
 // the K/V segment of every attention layer (either part can be skipped).
-// Each thread moves kSnapUnroll x 16 B.
-constexpr int kSnapUnroll = 4;
+// Each thread moves kSnapUnroll x 16 B (one piece per thread and many small
+// workgroups stream best).
+constexpr int kSnapUnroll = 1;
 __device__ __forceinline__ int64_t snap_units_begin(const SnapshotArgs& a) {
     return a.do_state ? 0 : a.state_bytes / 16;
 }
