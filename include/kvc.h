@@ -65,6 +65,12 @@ enum { KVC_DTYPE_F32 = 0, KVC_DTYPE_BF16 = 1 };
 /* Test hook: keep 4 bits of the block hash so collisions are frequent; token
  * verification must still reject every false match. */
 #define KVC_FLAG_WEAK_HASH 0x1u
+/* Decode work split (tuning and test hooks).  By default a decode launch with
+ * fewer than 256 (kv head, chunk) items splits each chunk's 256 output dims
+ * over two workgroups; these force the split always or never.  They exclude
+ * each other. */
+#define KVC_FLAG_DECODE_SPLIT_D 0x2u
+#define KVC_FLAG_DECODE_NO_SPLIT_D 0x4u
 
 typedef struct kvc_config {
     int32_t n_attn_layers;     /* full-attention layers (8, model_config.h:8,34) */

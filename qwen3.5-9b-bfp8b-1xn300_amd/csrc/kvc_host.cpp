@@ -487,6 +487,8 @@ int kvc_create(const kvc_config* cfg, kvc_ctx** out) {
     if (k.snapshot_interval < 0 || (k.snapshot_interval % k.block_tokens) != 0)
         return set_err(KVC_ERR_INVALID, "snapshot_interval must be a non-negative multiple of block_tokens");
     if (k.snapshot_slots < 0) return set_err(KVC_ERR_INVALID, "snapshot_slots must be >= 0");
+    if ((k.flags & KVC_FLAG_DECODE_SPLIT_D) && (k.flags & KVC_FLAG_DECODE_NO_SPLIT_D))
+        return set_err(KVC_ERR_INVALID, "KVC_FLAG_DECODE_SPLIT_D and KVC_FLAG_DECODE_NO_SPLIT_D exclude each other");
     if (k.n_ssm_layers > 0 &&
         (k.ssm_v_heads <= 0 || k.ssm_k_dim <= 0 || k.ssm_v_dim <= 0 || k.conv_rows <= 0 || k.conv_channels <= 0))
         return set_err(KVC_ERR_INVALID, "recurrent-state shape must be positive");
@@ -522,7 +524,7 @@ int kvc_create(const kvc_config* cfg, kvc_ctx** out) {
         }
         const size_t table_bytes = (size_t)k.max_seqs * c->max_blocks * 4;
         const size_t part_bytes = kPartBytes;
-        const size_t ctr_bytes = (size_t)kMaxBatch * kKvHeads * 4;
+        const size_t ctr_bytes = (size_t)kMaxBatch * kKvHeads * kMaxDParts * kCounterStride * 4;
         if ((rc = dev_alloc(c, (void**)&c->d_table, table_bytes, "block table")) ||
             (rc = dev_alloc(c, (void**)&c->d_state, (size_t)c->state_bytes * k.max_seqs, "state pool")) ||
             (rc = dev_alloc(c, (void**)&c->d_snap, (size_t)c->snap_bytes * n_snap, "snapshot pool")) ||
@@ -913,6 +915,10 @@ int kvc_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
     return KVC_OK;
 }
 
+// Decode launches with fewer work items than this split each chunk's output
+// dims over 2 workgroups (one per CU of the 256 is the aim).
+constexpr int64_t kDsplitBelowItems = 256;
+
 static int32_t auto_chunk_blocks(kvc_ctx* c, int64_t total_blocks) {
     if (c->cfg.decode_chunk_blocks > 0) return c->cfg.decode_chunk_blocks;
     // ~4 workgroups per CU on 256 CUs; chunks of at least 4 blocks keep the
@@ -948,6 +954,8 @@ int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
             total_blocks += (L + kBlockTok - 1) / kBlockTok;
         }
         int32_t cb = auto_chunk_blocks(c, total_blocks);
+        const bool force_split = c->cfg.flags & KVC_FLAG_DECODE_SPLIT_D;
+        const int64_t max_chunks = force_split ? kMaxChunks / kMaxDParts : kMaxChunks;
         int64_t total_chunks;
         for (;;) {
             total_chunks = 0;
@@ -956,9 +964,13 @@ int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
                 const int32_t nb = (a.kv_len[j] + kBlockTok - 1) / kBlockTok;
                 total_chunks += (nb + cb - 1) / cb;
             }
-            if (total_chunks <= kMaxChunks) break;
+            if (total_chunks <= max_chunks) break;
             cb *= 2;
         }
+        int32_t d_parts = 1;
+        if (force_split ||
+            (!(c->cfg.flags & KVC_FLAG_DECODE_NO_SPLIT_D) && total_chunks * kKvHeads < kDsplitBelowItems))
+            d_parts = 2;
         a.chunk_begin[n] = (int32_t)total_chunks;
         a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
         a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
@@ -976,7 +988,8 @@ int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
         a.n_seqs = n;
         a.chunk_blocks = cb;
         a.total_chunks = (int32_t)total_chunks;
-        a.n_items = (int32_t)(total_chunks * kKvHeads);
+        a.d_parts = d_parts;
+        a.n_items = (int32_t)(total_chunks * kKvHeads * d_parts);
         a.per_xcd = (a.n_items + 7) / 8;
         int e = launch_decode(a, stream);
         if (e) return hip_err((hipError_t)e, "decode launch");

@@ -36,6 +36,8 @@ constexpr int kMaxChunks = 8192;     // split-K work chunks per decode launch
 // split-K partial of one work item: acc [4 q heads][256] fp32 then (m, l) per
 // head, padded to whole 128-B lines so no line is shared by two items
 constexpr int kItemFloats = 1056;
+constexpr int kMaxDParts = 2;        // output-dim parts per decode chunk
+constexpr int kCounterStride = 32;   // int32s between arrival counters (one 128-B line each)
 constexpr size_t kPartBytes = (size_t)kMaxChunks * kKvHeads * kItemFloats * 4;
 constexpr int kTableUpdatesPerLaunch = 480;
 
@@ -59,15 +61,17 @@ struct DecodeArgs {
     const uint16_t* gate;   // [n_seqs][Hq][D] or null
     void* out;              // [n_seqs][Hq][D]
     float* part;            // split-K workspace [item][G][D + 2]
-    int32_t* counters;      // [kMaxBatch][Hkv] arrival counters (self-resetting)
+    int32_t* counters;      // [kMaxBatch][Hkv][kMaxDParts] arrival counters, kCounterStride
+                            // apart (self-resetting)
     float scale_log2;       // scale * log2(e)
     int32_t out_bf16;
     int32_t table_stride;   // max blocks per seq
     int32_t n_seqs;
     int32_t chunk_blocks;   // blocks per split-K chunk
     int32_t total_chunks;   // sum over seqs
-    int32_t n_items;        // total_chunks * Hkv
+    int32_t n_items;        // total_chunks * Hkv * d_parts
     int32_t per_xcd;        // ceil(n_items / 8)
+    int32_t d_parts;        // output-dim parts per (chunk, head): 1 or 2
     int32_t slot[kMaxBatch];
     int32_t kv_len[kMaxBatch];       // keys attended (new token included)
     int32_t chunk_begin[kMaxBatch + 1];

@@ -32,12 +32,16 @@ struct WaveState {
 };
 
 // One block's K/V as held by one wave (the wave owns 8 of the block's 32
-// tokens).  Lane = 16*ts + c (ts = 0..3, c = 0..15):
+// tokens) of a workgroup that produces output dims part dpart of NP (NP = 1:
+// all 256 dims; NP = 2: 128).  Lane = 16*ts + c (ts = 0..3, c = 0..15):
 //   k[2r + j]: token 4r + ts of the wave's 8, dims (c + 16j)*8 .. +7 (16 B)
-//   v[t]:      token t of the wave's 8, dims lane*4 .. lane*4+3 (8 B)
+//   v[i]:      token tsub*(8/NP) + i of the wave's 8, dims
+//              dpart*256/NP + dl*4 .. +3 (8 B), with dl = lane % (64/NP) and
+//              tsub = lane / (64/NP); NP = 1 gives token i, dims lane*4 ..
+template <int NP>
 struct BlockRegs {
     uint4 k[4];
-    uint2 v[kTokPerWave];
+    uint2 v[kTokPerWave / NP];
 };
 
 __device__ __forceinline__ void init_state(WaveState& st) {
@@ -53,25 +57,34 @@ __device__ __forceinline__ void init_state(WaveState& st) {
 
 // Load the wave's share of one (block, kv_head) unit with unconditional
 // 16-B / 8-B loads (every slot of an allocated unit is addressable; slots past
-// the sequence end are masked in compute_block).
-__device__ __forceinline__ void load_block(BlockRegs& r, const uint16_t* __restrict__ ku,
-                                           const uint16_t* __restrict__ vu, int wave, int lane) {
+// the sequence end are masked in compute_block).  With NP > 1 the sibling
+// workgroups of a chunk (same XCD, dispatched together) all read its K, so K
+// is loaded to stay in L2; V, read once, streams past it.
+template <int NP>
+__device__ __forceinline__ void load_block(BlockRegs<NP>& r, const uint16_t* __restrict__ ku,
+                                           const uint16_t* __restrict__ vu, int wave, int lane, int dpart) {
     const int ts = lane >> 4, c = lane & 15;
 #pragma unroll
     for (int rr = 0; rr < 2; rr++) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int t = wave * kTokPerWave + rr * 4 + ts;
-            const u32x4 y = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(ku + t * kHeadDim + (c + 16 * j) * 8));
-            r.k[rr * 2 + j] = make_uint4(y[0], y[1], y[2], y[3]);
+            const uint16_t* src = ku + t * kHeadDim + (c + 16 * j) * 8;
+            if constexpr (NP == 1) {
+                const u32x4 y = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+                r.k[rr * 2 + j] = make_uint4(y[0], y[1], y[2], y[3]);
+            } else {
+                r.k[rr * 2 + j] = *reinterpret_cast<const uint4*>(src);
+            }
         }
     }
+    constexpr int kLanesD = 64 / NP, kTokL = kTokPerWave / NP;
+    const int dl = lane % kLanesD, tsub = lane / kLanesD;
 #pragma unroll
-    for (int t = 0; t < kTokPerWave; t++) {
-        const u32x2 y = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x2*>(vu + (wave * kTokPerWave + t) * kHeadDim + lane * 4));
-        r.v[t] = make_uint2(y[0], y[1]);
+    for (int i = 0; i < kTokL; i++) {
+        const u32x2 y = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(
+            vu + (wave * kTokPerWave + tsub * kTokL + i) * kHeadDim + dpart * (kHeadDim / NP) + dl * 4));
+        r.v[i] = make_uint2(y[0], y[1]);
     }
 }
 
@@ -110,7 +123,8 @@ __device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(cv
 // Scores, online softmax update and P.V for one block held in registers.
 // qv[g][j][i]: packed bf16 pairs of q head g, dims (c + 16j)*8 + 2i, +1.
 // lds_p16: per-wave 32 bf16 p values laid out [g][token].
-__device__ __forceinline__ void compute_block(BlockRegs& r, const uint32_t (&qv)[kGroup][2][4],
+template <int NP>
+__device__ __forceinline__ void compute_block(BlockRegs<NP>& r, const uint32_t (&qv)[kGroup][2][4],
                                               int n_valid, float scale_log2, uint16_t* lds_p16,
                                               WaveState& st, int wave, int lane) {
     const int ts = lane >> 4, c = lane & 15;
@@ -191,18 +205,34 @@ __device__ __forceinline__ void compute_block(BlockRegs& r, const uint32_t (&qv)
     wave_lds_sync();
     if ((c & 1) == 0) lds_p16[my_g * kTokPerWave + t_loc] = (uint16_t)(__float_as_uint(p) >> 16);
     wave_lds_sync();
-    uint4 pp[kGroup];  // pp[g].{x,y,z,w} = (p[g][2k], p[g][2k+1]) for k = 0..3
+    // this lane's tokens t0 .. t0 + 8/NP - 1 of the wave's 8; pw[g][k] =
+    // (p[g][t0 + 2k], p[g][t0 + 2k + 1])
+    constexpr int kTokL = kTokPerWave / NP;
+    const int t0 = (lane / (64 / NP)) * kTokL;
+    uint32_t pw[kGroup][kTokL / 2];
 #pragma unroll
-    for (int g = 0; g < kGroup; g++) pp[g] = *reinterpret_cast<const uint4*>(lds_p16 + g * kTokPerWave);
+    for (int g = 0; g < kGroup; g++) {
+        if constexpr (NP == 1) {
+            const uint4 x = *reinterpret_cast<const uint4*>(lds_p16 + g * kTokPerWave);
+            pw[g][0] = x.x;
+            pw[g][1] = x.y;
+            pw[g][2] = x.z;
+            pw[g][3] = x.w;
+        } else {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(lds_p16 + g * kTokPerWave + t0);
+#pragma unroll
+            for (int k = 0; k < kTokL / 2; k++) pw[g][k] = src[k];
+        }
+    }
 
     if (n_valid < (wave + 1) * kTokPerWave) {  // partial block: stale slots may hold NaN bits
 #pragma unroll
-        for (int t = 0; t < kTokPerWave; t++)
-            if (wave * kTokPerWave + t >= n_valid) r.v[t] = make_uint2(0, 0);
+        for (int i = 0; i < kTokL; i++)
+            if (wave * kTokPerWave + t0 + i >= n_valid) r.v[i] = make_uint2(0, 0);
     }
     // P.V on token pairs with v_dot2_f32_bf16: (v[2k][d], v[2k+1][d]) packed
 #pragma unroll
-    for (int k = 0; k < kTokPerWave / 2; k++) {
+    for (int k = 0; k < kTokL / 2; k++) {
         const uint2 v0 = r.v[2 * k], v1 = r.v[2 * k + 1];
         uint32_t vp[4];
         vp[0] = __builtin_amdgcn_perm(v1.x, v0.x, 0x05040100u);
@@ -211,9 +241,8 @@ __device__ __forceinline__ void compute_block(BlockRegs& r, const uint32_t (&qv)
         vp[3] = __builtin_amdgcn_perm(v1.y, v0.y, 0x07060302u);
 #pragma unroll
         for (int g = 0; g < kGroup; g++) {
-            const uint32_t pk = k == 0 ? pp[g].x : k == 1 ? pp[g].y : k == 2 ? pp[g].z : pp[g].w;
 #pragma unroll
-            for (int j = 0; j < 4; j++) st.acc[g][j] = dot2_bf16(pk, vp[j], st.acc[g][j]);
+            for (int j = 0; j < 4; j++) st.acc[g][j] = dot2_bf16(pw[g][k], vp[j], st.acc[g][j]);
         }
     }
 }
@@ -340,21 +369,22 @@ __device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpoo
 // reads while the other stays in flight); a window's last 1-3 blocks take a
 // straight-line tail of their own, so no load is ever issued for a block that
 // is not computed.
+template <int NP>
 __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
                                             const uint16_t* __restrict__ vpool,
                                             const int32_t* __restrict__ trow, int h, int blk0,
                                             int n_blk, int L, const uint32_t (&qv)[kGroup][2][4],
                                             float scale_log2, uint16_t* lds_p, WaveState& st,
-                                            int wave, int lane) {
-    BlockRegs r0, r1;
+                                            int wave, int lane, int dpart) {
+    BlockRegs<NP> r0, r1;
     constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
 #define KVC_LOAD_WIN(R, I)                                                                          \
     {                                                                                               \
         const size_t off_ = ((size_t)__builtin_amdgcn_readlane(my_id, (I)) * kKvHeads + h) * kUnitElems; \
-        load_block(R, kpool + off_, vpool + off_, wave, lane);                                     \
+        load_block<NP>(R, kpool + off_, vpool + off_, wave, lane, dpart);                          \
     }
 #define KVC_NV(I) min(kBlockTok, L - (blk0 + w0 + (I)) * kBlockTok)
-#define KVC_COMPUTE(R, I) compute_block(R, qv, KVC_NV(I), scale_log2, lds_p, st, wave, lane)
+#define KVC_COMPUTE(R, I) compute_block<NP>(R, qv, KVC_NV(I), scale_log2, lds_p, st, wave, lane)
     for (int w0 = 0; w0 < n_blk; w0 += 64) {
         const int wn = min(64, n_blk - w0);
         const int my_id = lane < wn ? trow[blk0 + w0 + lane] : 0;
@@ -394,10 +424,12 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
 
 // Fold one extra key (the fused-append token, bf16 rows knew/vnew of this kv
 // head) into a wave's finalized state (uniform m, l).  Each group of 16 lanes
-// holds all 256 dims of q.
+// holds all 256 dims of q.  Every lane rescales its acc; only the lanes of
+// token subset 0 add p * v (the subsets are summed afterwards).
+template <int NP>
 __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[kGroup][2][4],
                                            const uint16_t* knew, const uint16_t* vnew,
-                                           float scale_log2, int lane) {
+                                           float scale_log2, int lane, int dpart) {
     const int c = lane & 15;
     const uint4 k0 = *reinterpret_cast<const uint4*>(knew + c * 8);
     const uint4 k1 = *reinterpret_cast<const uint4*>(knew + (c + 16) * 8);
@@ -418,8 +450,11 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
         x += dpp<kDppRowRor8>(x);
         sc[g] = readlane(x, 0) * scale_log2;
     }
-    const uint2 v = *reinterpret_cast<const uint2*>(vnew + lane * 4);
-    const float vf[4] = {bf16lo(v.x), bf16hi(v.x), bf16lo(v.y), bf16hi(v.y)};
+    constexpr int kLanesD = 64 / NP;
+    const int dl = lane % kLanesD;
+    const float vs = lane < kLanesD ? 1.f : 0.f;
+    const uint2 v = *reinterpret_cast<const uint2*>(vnew + dpart * (kHeadDim / NP) + dl * 4);
+    const float vf[4] = {bf16lo(v.x) * vs, bf16hi(v.x) * vs, bf16lo(v.y) * vs, bf16hi(v.y) * vs};
 #pragma unroll
     for (int g = 0; g < kGroup; g++) {
         const float mn = fmaxf(st.m[g], sc[g]);
@@ -434,10 +469,14 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
 
 // ---------------------------------------------------------------------------
 // Split-K GQA decode.  Work item = (kv head, chunk of chunk_blocks blocks of
-// one sequence); items of one (seq, head) are consecutive and are spread over
-// the 8 XCDs in contiguous runs (workgroup b runs on XCD b % 8).  Each item
-// writes (m, l, acc) for its 4 q heads; the last item of a (seq, head) to
-// arrive (device-scope counter) combines them and writes the output.
+// one sequence, output-dim part); items of one (seq, head) are consecutive
+// and are spread over the 8 XCDs in contiguous runs (workgroup b runs on XCD
+// b % 8), so the NP parts of a chunk share an XCD and its L2.  Each item
+// writes (m, l, acc) for its 4 q heads and its 256/NP dims; the last item of
+// a (seq, head, part) to arrive (device-scope counter) combines them and
+// writes the output.  NP = 2 is used when one part per chunk would leave CUs
+// idle: it doubles the workgroups and halves what each combiner pulls, at
+// the price of a second (L2-served) read of each chunk's K.
 constexpr int kCombineBatch = 32;
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -489,13 +528,17 @@ __device__ __forceinline__ void combine_batch(__amdgpu_buffer_rsrc_t prs, int it
     }
 }
 
+template <int NP>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     __shared__ DecodeSmem sm;
+    constexpr int kLanesD = 64 / NP;  // lanes per token subset
     const int b = blockIdx.x;
     const int item = (b & 7) * a.per_xcd + (b >> 3);
     if (item >= a.n_items) return;
-    const int h = item / a.total_chunks;
-    const int chunk = item - h * a.total_chunks;
+    const int dpart = item % NP;
+    const int hc = item / NP;
+    const int h = hc / a.total_chunks;
+    const int chunk = hc - h * a.total_chunks;
     int s = 0;
     while (s + 1 < a.n_seqs && a.chunk_begin[s + 1] <= chunk) s++;
     const int c = chunk - a.chunk_begin[s];
@@ -517,39 +560,88 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     init_state(st);
     // keys [0, Lw) come from the pool; with a fused append the last key
     // (position L-1) comes from knew/vnew and is folded in by wave 0 of the
-    // chunk that owns it, which also writes it into the pool
+    // chunk that owns it, whose part 0 also writes it into the pool
     const int Lw = a.k_new ? L - 1 : L;
     const int wblk1 = min(blk1, (Lw + kBlockTok - 1) / kBlockTok);
-    walk_blocks(a.kpool, a.vpool, trow, h, blk0, max(0, wblk1 - blk0), Lw, qv, a.scale_log2, sm.p16[wave], st,
-                wave, lane);
+    walk_blocks<NP>(a.kpool, a.vpool, trow, h, blk0, max(0, wblk1 - blk0), Lw, qv, a.scale_log2, sm.p16[wave],
+                    st, wave, lane, dpart);
     finalize_l(st);
     const bool owns_new = new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
     if (owns_new) {
-        if (wave == 0) fold_token(st, qv, knew, vnew, a.scale_log2, lane);
-        append_new_token(const_cast<uint16_t*>(a.kpool), const_cast<uint16_t*>(a.vpool), trow, h, new_pos,
-                         knew, vnew);
+        if (wave == 0) fold_token<NP>(st, qv, knew, vnew, a.scale_log2, lane, dpart);
+        if (dpart == 0)
+            append_new_token(const_cast<uint16_t*>(a.kpool), const_cast<uint16_t*>(a.vpool), trow, h, new_pos,
+                             knew, vnew);
     }
 
+    const int t = threadIdx.x, g = t >> 6;
     float M, Lsum, A[4];
-    merge_waves(st, sm, wave, lane, M, Lsum, A);
-    const int t = threadIdx.x, g = t >> 6, d0 = (t & 63) * 4;
+    int d0;
+    bool act = true;  // this thread holds output dims d0 .. d0 + 3
+    if constexpr (NP == 1) {
+        merge_waves(st, sm, wave, lane, M, Lsum, A);
+        d0 = (t & 63) * 4;
+    } else {
+        // sum the token subsets of each dim (lanes l and l ^ 32), then merge
+        // the 4 waves through LDS; lanes dl < 32 hold dims dpart*128 + dl*4
+#pragma unroll
+        for (int gg = 0; gg < kGroup; gg++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) st.acc[gg][j] = sum_xor32(st.acc[gg][j]);
+        static_assert(NP == 2, "d-split decode is built for 2 parts");
+        const int dl = lane % kLanesD;
+        act = lane < kLanesD;
+        if (act) {
+#pragma unroll
+            for (int gg = 0; gg < kGroup; gg++)
+                *reinterpret_cast<float4*>(&sm.acc[wave][gg][dl * 4]) =
+                    make_float4(st.acc[gg][0], st.acc[gg][1], st.acc[gg][2], st.acc[gg][3]);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int gg = 0; gg < kGroup; gg++) {
+                sm.ml[wave][gg][0] = st.m[gg];
+                sm.ml[wave][gg][1] = st.l[gg];
+            }
+        }
+        __syncthreads();
+        M = kNegBig;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, sm.ml[w][g][0]);
+        Lsum = 0.f;
+        A[0] = A[1] = A[2] = A[3] = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float wt = fast_exp2(sm.ml[w][g][0] - M);
+            Lsum = fmaf(wt, sm.ml[w][g][1], Lsum);
+            const float4 x = *reinterpret_cast<const float4*>(&sm.acc[w][g][dl * 4]);
+            A[0] = fmaf(wt, x.x, A[0]);
+            A[1] = fmaf(wt, x.y, A[1]);
+            A[2] = fmaf(wt, x.z, A[2]);
+            A[3] = fmaf(wt, x.w, A[3]);
+        }
+        d0 = dpart * (kHeadDim / NP) + dl * 4;
+    }
     const size_t orow = ((size_t)s * kQHeads + h * kGroup + g) * kHeadDim;
     const uint16_t* grow = a.gate ? a.gate + orow : nullptr;
     if (n_chunks == 1) {
-        write_out(a.out, a.out_bf16, orow, d0, grow, Lsum, A);
+        if (act) write_out(a.out, a.out_bf16, orow, d0, grow, Lsum, A);
         return;
     }
     // publish (m, l, acc) with agent-coherent 16-B stores; once they have all
     // completed (s_waitcnt 0) the arrival counter is bumped.  The last item of
-    // (s, h) to arrive reads the partials back with agent-coherent loads.
+    // (s, h, part) to arrive reads the partials back with agent-coherent loads.
     const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.part, (uint32_t)kPartBytes);
     const int ibase = item * kItemFloats * 4;
-    u32x4 av;
-    av[0] = __float_as_uint(A[0]);
-    av[1] = __float_as_uint(A[1]);
-    av[2] = __float_as_uint(A[2]);
-    av[3] = __float_as_uint(A[3]);
-    __builtin_amdgcn_raw_buffer_store_b128(av, prs, ibase + (g * kHeadDim + d0) * 4, 0, kCpolSC1);
+    const int aoff = g * kHeadDim + (d0 - dpart * (kHeadDim / NP));  // acc slot of this thread's dims
+    if (act) {
+        u32x4 av;
+        av[0] = __float_as_uint(A[0]);
+        av[1] = __float_as_uint(A[1]);
+        av[2] = __float_as_uint(A[2]);
+        av[3] = __float_as_uint(A[3]);
+        __builtin_amdgcn_raw_buffer_store_b128(av, prs, ibase + aoff * 4, 0, kCpolSC1);
+    }
     if ((t & 63) == 0) {
         u32x2 mlv;
         mlv[0] = __float_as_uint(M);
@@ -558,29 +650,72 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    // one 128-B line per counter: arrivals on different counters do not
+    // contend for one line
+    int32_t* ctr = a.counters + ((s * kKvHeads + h) * kMaxDParts + dpart) * kCounterStride;
     if (t == 0) {
-        const int prev = __hip_atomic_fetch_add(&a.counters[s * kKvHeads + h], 1, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
+        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         sm.last = (prev == n_chunks - 1);
     }
     __syncthreads();
     if (!sm.last) return;
-    // combine the n_chunks partials of (s, h): wave g takes q head g; every
-    // partial of a batch is requested at once (lane k also fetches partial
-    // k's (m, l)), then the acc rows are folded in arrival order
-    const int first = h * a.total_chunks + a.chunk_begin[s];
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < n_chunks; k0 += kCombineBatch) {
-        const int nk = min(kCombineBatch, n_chunks - k0);
-        if (nk <= 8)
-            combine_batch<8>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
-        else if (nk <= 16)
-            combine_batch<16>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
-        else
-            combine_batch<32>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
+    if constexpr (NP == 1) {
+        // combine the n_chunks partials of (s, h): wave g takes q head g; every
+        // partial of a batch is requested at once (lane k also fetches partial
+        // k's (m, l)), then the acc rows are folded in arrival order
+        const int first = h * a.total_chunks + a.chunk_begin[s];
+        for (int k0 = 0; k0 < n_chunks; k0 += kCombineBatch) {
+            const int nk = min(kCombineBatch, n_chunks - k0);
+            if (nk <= 8)
+                combine_batch<8>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
+            else if (nk <= 16)
+                combine_batch<16>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
+            else
+                combine_batch<32>(prs, first + k0, nk, g, d0, lane, Mc, Lc, Ac);
+        }
+    } else {
+        // wave g takes q head g; lane = psub * 32 + dl folds chunks k0 + 2k +
+        // psub of dims dl*4 .. +3 of this part; lane j also fetches chunk
+        // k0 + j's (m, l), so the batch max and the weights come from wave
+        // reductions and only the acc rows are summed over the two lane halves
+        const int psub = lane / kLanesD, dl = lane % kLanesD;
+        const int first = (h * a.total_chunks + a.chunk_begin[s]) * NP + dpart;
+        constexpr int kNB = kCombineBatch / NP;
+        for (int k0 = 0; k0 < n_chunks; k0 += kCombineBatch) {
+            const int nk = min(kCombineBatch, n_chunks - k0);
+            const int kl = min(lane, nk - 1);
+            const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(
+                prs, ((first + (k0 + kl) * NP) * kItemFloats + kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
+            u32x4 pa[kNB];
+#pragma unroll
+            for (int k = 0; k < kNB; k++) {
+                const int cc = min(k0 + k * NP + psub, n_chunks - 1);
+                pa[k] = __builtin_amdgcn_raw_buffer_load_b128(
+                    prs, ((first + cc * NP) * kItemFloats + g * kHeadDim + dl * 4) * 4, 0, kCpolSC1);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
+            const bool own = lane < nk;
+            const float m_l = own ? __uint_as_float(ml[0]) : kNegBig;
+            const float mb = fmaxf(Mc, wave_max(m_l));
+            const float cs = fast_exp2(Mc - mb);
+            Mc = mb;
+            const float w_l = own ? fast_exp2(m_l - mb) : 0.f;  // 0 for chunks past nk
+            Lc = fmaf(Lc, cs, wave_sum(w_l * __uint_as_float(ml[1])));
+#pragma unroll
+            for (int j = 0; j < 4; j++) Ac[j] *= cs;
+#pragma unroll
+            for (int k = 0; k < kNB; k++) {
+                const float w = psub ? readlane(w_l, k * NP + 1) : readlane(w_l, k * NP);
+#pragma unroll
+                for (int j = 0; j < 4; j++) Ac[j] = fmaf(w, __uint_as_float(pa[k][j]), Ac[j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) Ac[j] = sum_xor32(Ac[j]);
     }
-    write_out(a.out, a.out_bf16, orow, d0, grow, Lc, Ac);
-    if (t == 0) a.counters[s * kKvHeads + h] = 0;
+    if (act) write_out(a.out, a.out_bf16, orow, d0, grow, Lc, Ac);
+    if (t == 0) *ctr = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1114,7 +1249,10 @@ int launch_table_update(const TableUpdateArgs& a, void* stream) {
 
 int launch_decode(const DecodeArgs& a, void* stream) {
     const int grid = a.per_xcd * 8;
-    hipLaunchKernelGGL(decode_kernel, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
+    if (a.d_parts == 2)
+        hipLaunchKernelGGL(decode_kernel<2>, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(decode_kernel<1>, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 

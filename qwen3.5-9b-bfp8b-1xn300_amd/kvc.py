@@ -33,6 +33,8 @@ ERR_NAMES = {
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 FLAG_WEAK_HASH = 0x1
+FLAG_DECODE_SPLIT_D = 0x2
+FLAG_DECODE_NO_SPLIT_D = 0x4
 
 # every symbol include/kvc.h declares
 EXPORTS = [

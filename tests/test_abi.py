@@ -50,6 +50,9 @@ def test_unsupported_shapes_rejected():
     with pytest.raises(kvc.KvcError) as e:
         host_ctx(pool_blocks=0)
     assert e.value.code == kvc.KVC_ERR_INVALID
+    with pytest.raises(kvc.KvcError) as e:
+        host_ctx(flags=kvc.FLAG_DECODE_SPLIT_D | kvc.FLAG_DECODE_NO_SPLIT_D)
+    assert e.value.code == kvc.KVC_ERR_INVALID
 
 
 def test_device_ops_fail_loudly_on_host_only_context():

@@ -19,6 +19,10 @@ pytestmark = pytest.mark.gpu
 LAYERS = 2
 
 
+# decode work split: automatic, forced on (two output-dim parts per chunk) or off
+SPLIT_FLAGS = {"auto": 0, "on": kvc.FLAG_DECODE_SPLIT_D, "off": kvc.FLAG_DECODE_NO_SPLIT_D}
+
+
 def make_ctx(**over):
     cfg = dict(n_attn_layers=LAYERS, n_ssm_layers=0, max_seqs=16, max_seq_len=8192,
                pool_blocks=4096, snapshot_slots=0, snapshot_interval=256, alloc_seed=12345)
@@ -99,11 +103,12 @@ def test_decode_matches_golden(golden_dir, L):
         O.assert_attn_close(out, g[f"dec{L}_out"], rel_rms=3e-3, what=f"golden L={L} tight")
 
 
+@pytest.mark.parametrize("split", ["auto", "on", "off"])
 @pytest.mark.parametrize("chunk_blocks", [0, 1, 2, 5])
-def test_decode_batch_vs_oracle(chunk_blocks):
-    say(f"decode batch vs oracle chunk_blocks={chunk_blocks}")
+def test_decode_batch_vs_oracle(chunk_blocks, split):
+    say(f"decode batch vs oracle chunk_blocks={chunk_blocks} split={split}")
     lens = [1, 31, 32, 33, 100, 257, 1000, 2500]
-    with make_ctx(decode_chunk_blocks=chunk_blocks) as ctx:
+    with make_ctx(decode_chunk_blocks=chunk_blocks, flags=SPLIT_FLAGS[split]) as ctx:
         m = Mirror(1)
         seqs = [ctx.seq_create() for _ in lens]
         for s, L in zip(seqs, lens):
@@ -117,10 +122,11 @@ def test_decode_batch_vs_oracle(chunk_blocks):
             O.assert_attn_close(out[i], ref, rel_rms=3e-3, what='tight')
 
 
-def test_decode_fused_append_and_bf16_out():
-    say("fused append + bf16 output + gate")
+@pytest.mark.parametrize("split", ["on", "off"])
+def test_decode_fused_append_and_bf16_out(split):
+    say(f"fused append + bf16 output + gate, split={split}")
     lens = [63, 64, 65, 700]
-    with make_ctx() as ctx:
+    with make_ctx(flags=SPLIT_FLAGS[split]) as ctx:
         m = Mirror(LAYERS)
         seqs = [ctx.seq_create() for _ in lens]
         for s, L in zip(seqs, lens):
@@ -151,10 +157,11 @@ def test_decode_fused_append_and_bf16_out():
             assert np.array_equal(got[i][0], mk) and np.array_equal(got[i][1], mv)
 
 
-def test_decode_closed_forms():
-    say("decode closed forms: GQA map, identical keys")
+@pytest.mark.parametrize("split", ["on", "off"])
+def test_decode_closed_forms(split):
+    say(f"decode closed forms: GQA map, identical keys, split={split}")
     L = 96
-    with make_ctx() as ctx:
+    with make_ctx(flags=SPLIT_FLAGS[split]) as ctx:
         h = kvc.hip()
         s = ctx.seq_create()
         ctx.reserve([s], L)
@@ -244,13 +251,14 @@ def test_prefill_batch_vs_oracle():
             O.assert_attn_close(out[i], ref, rel_rms=3e-3, what='tight')
 
 
-def test_splitk_workspace_reuse_stress():
+@pytest.mark.parametrize("split", ["on", "off"])
+def test_splitk_workspace_reuse_stress(split):
     """Many split-K launches back to back on one stream, each with new data in
     the same partial workspace and arrival counters: every output must match
     the oracle (catches stale partials read across XCDs)."""
-    say("split-K workspace reuse stress")
+    say(f"split-K workspace reuse stress, split={split}")
     lens = [4096, 700, 1537]
-    with make_ctx(decode_chunk_blocks=1) as ctx:
+    with make_ctx(decode_chunk_blocks=1, flags=SPLIT_FLAGS[split]) as ctx:
         m = Mirror(1)
         seqs = [ctx.seq_create() for _ in lens]
         for s, L in zip(seqs, lens):
