@@ -907,9 +907,8 @@ int kvc_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
             a.slot[j] = seqs[i0 + j];
             a.pos0[j] = s.len + s.pending - n_tok;
         }
-        const int64_t units = (int64_t)2 * n * n_tok * kKvHeads * (kHeadDim * 2 / 16);
-        if (units > INT32_MAX) return set_err(KVC_ERR_RANGE, "append too large");
-        int e = launch_append(a, (int)units, stream);
+        if ((int64_t)n * n_tok > INT32_MAX) return set_err(KVC_ERR_RANGE, "append too large");
+        int e = launch_append(a, stream);
         if (e) return hip_err((hipError_t)e, "append launch");
     }
     return KVC_OK;

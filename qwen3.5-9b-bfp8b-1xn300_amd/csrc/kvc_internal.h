@@ -163,7 +163,7 @@ struct BlockCopyArgs {
 // ---- launchers (kvc_kernels.hip); return hipError_t as int ---------------
 int launch_table_update(const TableUpdateArgs& a, void* stream);
 int launch_decode(const DecodeArgs& a, void* stream);
-int launch_append(const AppendArgs& a, int n_units, void* stream);
+int launch_append(const AppendArgs& a, void* stream);
 int launch_gather(const GatherArgs& a, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_snapshot(const SnapshotArgs& a, void* stream);

@@ -1080,26 +1080,26 @@ void prefill_mfma_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Append: one thread per 16 bytes of a (token, kv head) row of K or V.
-__global__ __launch_bounds__(256) void append_kernel(AppendArgs a, int n_units) {
-    const int u = blockIdx.x * blockDim.x + threadIdx.x;  // 16-B unit
-    if (u >= n_units) return;
-    constexpr int kRowUnits = kHeadDim * 2 / 16;  // 32
-    const int part = u % kRowUnits;
-    const int row = u / kRowUnits;  // over [kv][seq][tok][head]
-    const int rows_per_kv = a.n_seqs * a.n_tok * kKvHeads;
-    const int kv = row / rows_per_kv;
-    const int r = row - kv * rows_per_kv;
-    const int h = r % kKvHeads;
-    const int tok = (r / kKvHeads) % a.n_tok;
-    const int s = r / (kKvHeads * a.n_tok);
+// Append: one workgroup per (sequence, token) moves that token's K and V rows
+// (4 heads x 512 B each); thread t copies 16 B: kv = t / 128, head =
+// (t / 32) % 4, piece = t % 32.  The sequence, position and block id are
+// workgroup-uniform (scalar), so no lane does index division.  The pool store
+// is non-temporal (streamed past L2): measured 11.9 us for 64 x 128 tokens
+// against 14.9 us with a plain store; more tokens per workgroup gained no more.
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+    const int b = blockIdx.x;
+    const int s = b / a.n_tok;
+    const int tok = b - s * a.n_tok;
     const int pos = a.pos0[s] + tok;
     const int blk = a.table[(size_t)a.slot[s] * a.table_stride + pos / kBlockTok];
+    const int t = threadIdx.x;
+    const int kv = t >> 7, h = (t >> 5) & 3, part = t & 31;
     const size_t dst = (((size_t)blk * kKvHeads + h) * kBlockTok + pos % kBlockTok) * kHeadDim + part * 8;
-    const size_t src = (size_t)r * kHeadDim + part * 8;
+    const size_t src = (((size_t)s * a.n_tok + tok) * kKvHeads + h) * kHeadDim + part * 8;
     const uint16_t* from = kv ? a.v : a.k;
     uint16_t* to = kv ? a.vpool : a.kpool;
-    *reinterpret_cast<uint4*>(to + dst) = *reinterpret_cast<const uint4*>(from + src);
+    const u32x4 x = *reinterpret_cast<const u32x4*>(from + src);
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(to + dst));
 }
 
 // Gather: work item = (sequence, 32 consecutive output tokens), split over 8
@@ -1262,9 +1262,9 @@ int launch_prefill(const PrefillArgs& a, void* stream) {
     return (int)hipGetLastError();
 }
 
-int launch_append(const AppendArgs& a, int n_units, void* stream) {
-    hipLaunchKernelGGL(append_kernel, dim3((n_units + 255) / 256), dim3(256), 0, (hipStream_t)stream,
-                       a, n_units);
+int launch_append(const AppendArgs& a, void* stream) {
+    static_assert(2 * kKvHeads * kHeadDim * 2 / 16 == 256, "one 16-B piece per thread of a 256-thread workgroup");
+    hipLaunchKernelGGL(append_kernel, dim3(a.n_seqs * a.n_tok), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
