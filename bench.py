@@ -399,6 +399,14 @@ def run_c(args):
     ctx.fill_normal_bf16(qb, nses * n_q * NQ * D, SEED + 30, 1.0, stream)
     ctx.fill_normal_bf16(kb, nses * n_q * ROW, SEED + 31, 1.0, stream)
     ctx.fill_normal_bf16(vb, nses * n_q * ROW, SEED + 32, 1.0, stream)
+    # attention projection rows (bf16, the reference's qkv layout) and q/k
+    # norm weights for the producer leg
+    qkv_row = NQ * 2 * D + 2 * ROW
+    qkv = h.malloc(nses * n_q * qkv_row * 2)
+    ctx.fill_normal_bf16(qkv, nses * n_q * qkv_row, SEED + 33, 1.0, stream)
+    wn = np.random.default_rng(SEED + 34).uniform(0.5, 1.5, (2, D)).astype(np.float32)
+    qn, kn_w = h.malloc(D * 4).upload(wn[0]), h.malloc(D * 4).upload(wn[1])
+    q2, g2 = h.malloc(nses * n_q * NQ * D * 2), h.malloc(nses * n_q * NQ * D * 2)
     ctx.reserve(sess, n_q, stream)
     for layer in range(layers):
         ctx.append(layer, sess, n_q, kb, vb, stream)
@@ -412,6 +420,9 @@ def run_c(args):
     lens_ = [int(x) for x in reused]
     legs = {
         "append": lambda: [ctx.append(l_, sess, n_q, kb, vb, stream) for l_ in range(layers)],
+        # q/k RMSNorm + RoPE + K/V append from the projection rows, q and gate out
+        "qkv_append": lambda: [ctx.qkv_append(l_, sess, n_q, qkv, qn, kn_w, q_out=q2, gate_out=g2,
+                                              in_dtype=kvc.DTYPE_BF16, stream=stream) for l_ in range(layers)],
         "gather": lambda: [ctx.gather(l_, sess, 0, lens_, kout, vout, stream) for l_ in range(layers)],
         "prefill": lambda: [ctx.prefill_attn(l_, sess, n_q, qb, ob, out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16,
                                              stream=stream) for l_ in range(layers)],
@@ -420,7 +431,7 @@ def run_c(args):
     e0, e1 = h.event(), h.event()
     for name, fn in legs.items():
         g_ = h.capture(stream, fn)
-        n_rep = reps * (10 if name == "append" else 1)
+        n_rep = reps * (10 if name in ("append", "qkv_append") else 1)
         h.graph_launch(g_, stream)  # warm-up
         h.record(e0, stream)
         for _ in range(n_rep):
@@ -430,17 +441,22 @@ def run_c(args):
         h.graph_destroy(g_)
     ap_us, g_us, p_us = leg_us["append"], leg_us["gather"], leg_us["prefill"]
     ap_bytes = 2 * 2 * nses * n_q * ROW * 2  # K and V rows, read + write
+    # producer: projection row read (bf16) + q, gate, K, V written (bf16)
+    qa_us = leg_us["qkv_append"]
+    qa_bytes = nses * n_q * (qkv_row * 2 + 2 * NQ * D * 2 + 2 * ROW * 2)
     g_bytes = 2 * 2 * tot_tok * ROW * 2  # K and V, read + write
     flops = float(sum(16384 * (128 * int(p_) + 8256) for p_ in P))  # causal-exact QK^T + PV
     p_bytes = int(sum(ROW * 2 * 2 * (int(p_) + n_q) for p_ in P)) + 2 * nses * n_q * NQ * D * 2
-    for b_ in (kout, vout, qb, kb, vb, ob):
+    for b_ in (kout, vout, qb, kb, vb, ob, qkv, qn, kn_w, q2, g2):
         b_.free()
     ctx.close()
     return {"workload": "c: 64 sessions, 8 seeded base streams, block-aligned reused prefix U[256,3072] + 128 "
-                        "unique tokens; append of the 128 new tokens, gather of the reused blocks and 128-token causal "
-                        "chunked prefill per layer",
+                        "unique tokens; append of the 128 new tokens (plain, and from bf16 projection rows with q/k "
+                        "RMSNorm + RoPE), gather of the reused blocks and 128-token causal chunked prefill per layer",
             "prefix_match_us_per_session": round(match_us, 1),
             "append_us_per_layer": round(ap_us, 1), "append_GBps": round(ap_bytes / (ap_us * 1e-6) / 1e9, 1),
+            "qkv_append_us_per_layer": round(qa_us, 1),
+            "qkv_append_GBps": round(qa_bytes / (qa_us * 1e-6) / 1e9, 1),
             "gather_us_per_layer": round(g_us, 1), "gather_GBps": round(g_bytes / (g_us * 1e-6) / 1e9, 1),
             "prefill_us_per_layer": round(p_us, 1),
             "prefill_TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 2),

@@ -12,6 +12,9 @@
  *                               commit, src/engine.cpp:3039, :4106, :4118, :4150-4151
  *   kvc_prefix_match            prefix reuse in generate(), src/engine.cpp:4058-4080
  *   kvc_append                  K/V append, src/engine.cpp:3521-3525 and :2885-2889
+ *   kvc_qkv_append              the attention producer feeding that append:
+ *                               q/k per-head RMSNorm + partial RoPE, then the
+ *                               append, src/engine.cpp:3485-3525 and :2846-2889
  *   kvc_decode_attn             GQA decode attention (+ fused append),
  *                               src/engine.cpp:3528-3564
  *   kvc_prefill_attn            per-token causal attention of a prefill batch,
@@ -47,7 +50,7 @@
 extern "C" {
 #endif
 
-#define KVC_ABI_VERSION 1
+#define KVC_ABI_VERSION 2
 
 enum {
     KVC_OK = 0,
@@ -95,6 +98,12 @@ typedef struct kvc_config {
     uint32_t flags;            /* KVC_FLAG_* */
     uint64_t alloc_seed;       /* 0: blocks handed out in order; else a seeded
                                   permutation of the free list */
+    float rms_norm_eps;        /* q/k per-head RMSNorm eps (1e-6, model_config.h:18) */
+    float rope_freq_base;      /* RoPE base (1e7, model_config.h:21) */
+    int32_t rope_dim;          /* rotated dims per head, pairs (p, p + rope_dim/2)
+                                  (64, model_config.h:22); 0 or a power of two
+                                  in [8, head_dim] */
+    int32_t reserved;          /* 0 */
 } kvc_config;
 
 typedef struct kvc_stats {
@@ -156,6 +165,22 @@ int kvc_prefix_match(kvc_ctx* ctx, int32_t seq, const int32_t* tokens,
 int kvc_append(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
                int32_t n_seqs, int32_t n_tok, const void* k, const void* v,
                void* stream);
+/* Attention producer + append (src/engine.cpp:3485-3525 decode, :2846-2889
+ * prefill).  qkv holds the attention projection row of n_tok tokens per seq,
+ * [n_seqs][n_tok][row] with row = Hq*2*D + 2*Hkv*D laid out as the
+ * reference's: [Hq][q | gate][D], then k [Hkv][D], then v [Hkv][D]; fp32 or
+ * bf16 by in_dtype.  For each token at its pending position (as kvc_append):
+ * q and k get per-head RMSNorm (x * 1/sqrt(mean(x^2) + eps) * w, weights
+ * q_norm / k_norm: device fp32 [D]) and partial NeoX RoPE over dims
+ * [0, rope_dim) with the pairs (p, p + rope_dim/2) at the token's position
+ * (cos/sin tables built at kvc_create the way src/engine.cpp:2408-2419 builds
+ * them); k and v are appended to layer's cache as bf16 (RNE); q and gate are
+ * written as bf16 [n_seqs][n_tok][Hq][D] to q_out / gate_out (either may be
+ * NULL), ready for kvc_prefill_attn / kvc_decode_attn. */
+int kvc_qkv_append(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
+                   int32_t n_seqs, int32_t n_tok, const void* qkv,
+                   int32_t in_dtype, const void* q_norm, const void* k_norm,
+                   void* q_out, void* gate_out, void* stream);
 /* One query token per seq.  q: bf16 [n_seqs][Hq][D].  Attends over
  * [0, len + pending).  If k_new/v_new (bf16 [n_seqs][Hkv][D]) are given, they
  * are first written at position len + pending - 1 (fused append; reserve 1

@@ -29,6 +29,19 @@
  *   conv_push            explicit three-step shift by hand
  *   deltanet_head_step   fp64 restatement of the delta rule (S <- S*a; S +=
  *                        k (beta (v - S k))^T) on random small heads
+ *   rope_tables          theta of pair p at pos 1 is base^(-2p/rope_dim)
+ *                        (p = 0, 16, 31 checked against the closed form in
+ *                        fp64); cos^2 + sin^2 = 1; pos 0 is the identity
+ *   rms_norm_head        constant input -> w; scale invariance (x and 3x);
+ *                        output RMS = 1 with unit weights; eps dominates a
+ *                        zero head (output 0)
+ *   rope_head            unit vector on pair p -> (cos, sin) of the table
+ *                        (sign and pairing); pair norms preserved; dims >=
+ *                        rope_dim untouched; rotating by positions a then b
+ *                        equals a + b to fp32 accuracy
+ *   qkv_produce          deinterleave: gate rows and v rows are copies of
+ *                        the input rows; q/k equal norm-then-rope of their
+ *                        rows (composition of the two pinned steps)
  * No function is "parity unpinned".
  */
 #include "kvc_oracle.h"
@@ -345,5 +358,62 @@ void orc_deltanet_head_step(float* state, int dv, int dk, const float* q,
             o = fmaf(row[j], q[j], o);
         }
         out[i] = o * out_scale;
+    }
+}
+
+/* ---------------------------------------------------------------------- */
+/* K producer: per-head RMSNorm + partial NeoX RoPE                         */
+
+void orc_rope_tables(int max_ctx, int rope_dim, float base, float* cos_t, float* sin_t) {
+    const int half = rope_dim / 2;
+    for (int pos = 0; pos < max_ctx; pos++) {
+        for (int p = 0; p < half; p++) {
+            const float freq = 1.0f / powf(base, 2.0f * p / rope_dim);
+            const float theta = pos * freq;
+            cos_t[(size_t)pos * half + p] = cosf(theta);
+            sin_t[(size_t)pos * half + p] = sinf(theta);
+        }
+    }
+}
+
+void orc_rms_norm_head(float* x, int d, const float* w, float eps) {
+    float ss = 0.0f;
+    for (int i = 0; i < d; i++) ss += x[i] * x[i];
+    const float r = 1.0f / sqrtf(ss / d + eps);
+    for (int i = 0; i < d; i++) x[i] = x[i] * r * w[i];
+}
+
+void orc_rope_head(float* x, int rope_dim, const float* cos_row, const float* sin_row) {
+    const int half = rope_dim / 2;
+    for (int p = 0; p < half; p++) {
+        const float x0 = x[p], x1 = x[p + half];
+        x[p] = x0 * cos_row[p] - x1 * sin_row[p];
+        x[p + half] = x1 * cos_row[p] + x0 * sin_row[p];
+    }
+}
+
+void orc_qkv_produce(const float* qkv, int n_q, int n_kv, int d, int rope_dim,
+                     const float* q_norm, const float* k_norm, float eps,
+                     const float* cos_row, const float* sin_row, float* q,
+                     float* gate, float* k, float* v) {
+    const float* krow = qkv + (size_t)n_q * 2 * d;
+    const float* vrow = krow + (size_t)n_kv * d;
+    for (int h = 0; h < n_q; h++) {
+        if (q) {
+            float* qh = q + (size_t)h * d;
+            memcpy(qh, qkv + (size_t)h * 2 * d, sizeof(float) * d);
+            orc_rms_norm_head(qh, d, q_norm, eps);
+            if (rope_dim > 0) orc_rope_head(qh, rope_dim, cos_row, sin_row);
+        }
+        if (gate) memcpy(gate + (size_t)h * d, qkv + (size_t)h * 2 * d + d, sizeof(float) * d);
+    }
+    for (int h = 0; h < n_kv; h++) {
+        if (k) {
+            float* kh = k + (size_t)h * d;
+            memcpy(kh, krow + (size_t)h * d, sizeof(float) * d);
+            orc_rms_norm_head(kh, d, k_norm, eps);
+            if (rope_dim > 0) orc_rope_head(kh, rope_dim, cos_row, sin_row);
+        }
+        if (v) memcpy(v + (size_t)h * d, vrow + (size_t)h * d, sizeof(float) * d);
     }
 }

@@ -91,6 +91,28 @@ void orc_hash_chain(const int32_t* tok, int n_blocks, int block, int weak,
 int orc_reuse_len(int lcp, int n_prompt, int block, int interval,
                   const uint8_t* snap, int n_snap, int has_ssm);
 
+/* ---- K producer: per-head RMSNorm + partial RoPE ------------------------ */
+/* RoPE tables, src/engine.cpp:2408-2419: for pos < max_ctx, p < rope_dim/2,
+ * freq = 1/powf(base, 2p/rope_dim), theta = pos*freq (fp32), cos_t/sin_t
+ * [max_ctx][rope_dim/2] = cosf/sinf(theta). */
+void orc_rope_tables(int max_ctx, int rope_dim, float base, float* cos_t, float* sin_t);
+/* Per-head RMSNorm in place, src/engine.cpp:3497-3512: ss = sum x^2 in index
+ * order (fp32), r = 1/sqrtf(ss/d + eps), x[i] = x[i]*r*w[i]. */
+void orc_rms_norm_head(float* x, int d, const float* w, float eps);
+/* Partial NeoX RoPE in place on dims [0, rope_dim), pairs (p, p+rope_dim/2),
+ * src/engine.cpp:2422-2432: x0' = x0 c - x1 s, x1' = x1 c + x0 s with the
+ * table row of the token's position. */
+void orc_rope_head(float* x, int rope_dim, const float* cos_row, const float* sin_row);
+/* The attention producer of one token, src/engine.cpp:3485-3519 (decode) and
+ * :2846-2883 (prefill): qkv row = [n_q][2][d] (q then gate of each head),
+ * then k [n_kv][d], then v [n_kv][d].  Outputs (fp32): q [n_q][d] normed with
+ * q_norm and roped, gate [n_q][d], k [n_kv][d] normed with k_norm and roped,
+ * v [n_kv][d]; any output may be NULL. */
+void orc_qkv_produce(const float* qkv, int n_q, int n_kv, int d, int rope_dim,
+                     const float* q_norm, const float* k_norm, float eps,
+                     const float* cos_row, const float* sin_row, float* q,
+                     float* gate, float* k, float* v);
+
 /* ---- recurrent state (snapshot semantics only) -------------------------- */
 /* Conv window push: rows shift toward oldest, x becomes newest,
  * src/engine.cpp:3228-3230. state [3][channels]. */

@@ -123,6 +123,7 @@ struct kvc_ctx {
     uint8_t* d_snap = nullptr;
     float* d_part = nullptr;
     int32_t* d_counters = nullptr;
+    float* d_rope = nullptr;  // RoPE cos [max_seq_len][rope_dim/2], then sin likewise
 
     std::vector<int32_t> refcnt;
     std::vector<int32_t> free_blocks;
@@ -447,6 +448,10 @@ void kvc_config_default(kvc_config* cfg) {
     cfg->device = 0;
     cfg->flags = 0;
     cfg->alloc_seed = 0;
+    cfg->rms_norm_eps = 1e-6f;
+    cfg->rope_freq_base = 1.0e7f;
+    cfg->rope_dim = 64;
+    cfg->reserved = 0;
 }
 
 static void free_device(kvc_ctx* c) {
@@ -457,6 +462,7 @@ static void free_device(kvc_ctx* c) {
     if (c->d_snap) (void)hipFree(c->d_snap);
     if (c->d_part) (void)hipFree(c->d_part);
     if (c->d_counters) (void)hipFree(c->d_counters);
+    if (c->d_rope) (void)hipFree(c->d_rope);
 }
 
 static int dev_alloc(kvc_ctx* c, void** p, size_t bytes, const char* what) {
@@ -471,6 +477,28 @@ static int dev_alloc(kvc_ctx* c, void** p, size_t bytes, const char* what) {
     }
     c->hbm_bytes += (int64_t)bytes;
     return KVC_OK;
+}
+
+// RoPE cos/sin tables for every position of a sequence, computed as the
+// reference precomputes them (src/engine.cpp:2408-2419: fp32 freq = 1 /
+// powf(base, 2p / rope_dim), theta = pos * freq, cosf / sinf) and uploaded
+// once.
+static int build_rope_table(kvc_ctx* c) {
+    const int half = c->cfg.rope_dim / 2;
+    const size_t n = (size_t)c->cfg.max_seq_len * half;
+    std::vector<float> tab(2 * n);
+    for (int pos = 0; pos < c->cfg.max_seq_len; pos++) {
+        for (int p = 0; p < half; p++) {
+            const float freq = 1.0f / powf(c->cfg.rope_freq_base, 2.0f * p / c->cfg.rope_dim);
+            const float theta = pos * freq;
+            tab[(size_t)pos * half + p] = cosf(theta);
+            tab[n + (size_t)pos * half + p] = sinf(theta);
+        }
+    }
+    int rc = dev_alloc(c, (void**)&c->d_rope, tab.size() * sizeof(float), "RoPE tables");
+    if (rc) return rc;
+    hipError_t e = hipMemcpy(c->d_rope, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
+    return e == hipSuccess ? KVC_OK : hip_err(e, "RoPE table upload");
 }
 
 int kvc_create(const kvc_config* cfg, kvc_ctx** out) {
@@ -492,6 +520,12 @@ int kvc_create(const kvc_config* cfg, kvc_ctx** out) {
     if (k.n_ssm_layers > 0 &&
         (k.ssm_v_heads <= 0 || k.ssm_k_dim <= 0 || k.ssm_v_dim <= 0 || k.conv_rows <= 0 || k.conv_channels <= 0))
         return set_err(KVC_ERR_INVALID, "recurrent-state shape must be positive");
+    if (k.rope_dim != 0 && (k.rope_dim < 8 || k.rope_dim > kHeadDim || (k.rope_dim & (k.rope_dim - 1)) != 0))
+        return set_err(KVC_ERR_UNSUPPORTED, "rope_dim must be 0 or a power of two in [8, %d] (got %d)", kHeadDim,
+                       k.rope_dim);
+    if (!(k.rope_freq_base > 0.0f) || !std::isfinite(k.rope_freq_base) || !(k.rms_norm_eps >= 0.0f) ||
+        !std::isfinite(k.rms_norm_eps))
+        return set_err(KVC_ERR_INVALID, "rope_freq_base must be positive and rms_norm_eps non-negative");
 
     kvc_ctx* c = new (std::nothrow) kvc_ctx();
     if (!c) return set_err(KVC_ERR_NOMEM, "host allocation failed");
@@ -565,6 +599,11 @@ int kvc_create(const kvc_config* cfg, kvc_ctx** out) {
             free_device(c);
             delete c;
             return hip_err(e, "initialising device tables");
+        }
+        if (k.rope_dim > 0 && (rc = build_rope_table(c))) {
+            free_device(c);
+            delete c;
+            return rc;
         }
     } else {
         if (k.pool_blocks <= 0 || k.pool_blocks > INT32_MAX) {
@@ -910,6 +949,52 @@ int kvc_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
         if ((int64_t)n * n_tok > INT32_MAX) return set_err(KVC_ERR_RANGE, "append too large");
         int e = launch_append(a, stream);
         if (e) return hip_err((hipError_t)e, "append launch");
+    }
+    return KVC_OK;
+}
+
+int kvc_qkv_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t n_tok, const void* qkv,
+                   int32_t in_dtype, const void* q_norm, const void* k_norm, void* q_out, void* gate_out,
+                   void* stream) {
+    if (!c) return set_err(KVC_ERR_INVALID, "null context");
+    int rc;
+    if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
+    if (!qkv || !q_norm || !k_norm || n_tok <= 0)
+        return set_err(KVC_ERR_INVALID, "qkv append needs qkv, q_norm, k_norm and n_tok > 0");
+    if (in_dtype != KVC_DTYPE_F32 && in_dtype != KVC_DTYPE_BF16) return set_err(KVC_ERR_INVALID, "bad in_dtype");
+    for (int32_t i = 0; i < n_seqs; i++)
+        if (c->seqs[seqs[i]].pending < n_tok)
+            return set_err(KVC_ERR_STATE, "sequence %d: append of %d tokens but %d reserved", seqs[i], n_tok,
+                           c->seqs[seqs[i]].pending);
+    const size_t esz = in_dtype == KVC_DTYPE_BF16 ? 2 : 4;
+    const size_t qrow = (size_t)kQHeads * kHeadDim;
+    for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+        const int32_t n = std::min(kMaxBatch, n_seqs - i0);
+        if ((int64_t)n * n_tok > INT32_MAX) return set_err(KVC_ERR_RANGE, "qkv append too large");
+        QkvArgs a{};
+        a.qkv = static_cast<const uint8_t*>(qkv) + (size_t)i0 * n_tok * kQkvRow * esz;
+        a.q_norm = static_cast<const float*>(q_norm);
+        a.k_norm = static_cast<const float*>(k_norm);
+        a.rope = c->d_rope;
+        a.kpool = reinterpret_cast<uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
+        a.vpool = reinterpret_cast<uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
+        a.table = c->d_table;
+        a.q_out = q_out ? static_cast<uint16_t*>(q_out) + (size_t)i0 * n_tok * qrow : nullptr;
+        a.gate_out = gate_out ? static_cast<uint16_t*>(gate_out) + (size_t)i0 * n_tok * qrow : nullptr;
+        a.eps = c->cfg.rms_norm_eps;
+        a.in_bf16 = in_dtype == KVC_DTYPE_BF16;
+        a.rope_half = c->cfg.rope_dim / 2;
+        a.rope_rows = c->cfg.max_seq_len;
+        a.table_stride = c->max_blocks;
+        a.n_seqs = n;
+        a.n_tok = n_tok;
+        for (int32_t j = 0; j < n; j++) {
+            const Seq& s = c->seqs[seqs[i0 + j]];
+            a.slot[j] = seqs[i0 + j];
+            a.pos0[j] = s.len + s.pending - n_tok;
+        }
+        int e = launch_qkv_append(a, stream);
+        if (e) return hip_err((hipError_t)e, "qkv append launch");
     }
     return KVC_OK;
 }

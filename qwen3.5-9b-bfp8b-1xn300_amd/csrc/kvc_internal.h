@@ -91,6 +91,31 @@ struct AppendArgs {
     int32_t pos0[kMaxBatch];  // first position written
 };
 
+// attention projection row of one token: [Hq][q | gate][D], k [Hkv][D], v [Hkv][D]
+constexpr int kQkvRow = kQHeads * 2 * kHeadDim + 2 * kKvHeads * kHeadDim;
+
+struct QkvArgs {
+    const void* qkv;        // [n_seqs][n_tok][kQkvRow], fp32 or bf16
+    const float* q_norm;    // [D]
+    const float* k_norm;    // [D]
+    const float* rope;      // cos [rope_rows][rope_half], then sin [rope_rows][rope_half]
+    uint16_t* kpool;
+    uint16_t* vpool;
+    const int32_t* table;
+    uint16_t* q_out;        // [n_seqs][n_tok][Hq][D] bf16 or null
+    uint16_t* gate_out;     // likewise
+    float eps;
+    int32_t in_bf16;
+    int32_t rope_half;      // rope_dim / 2 (0 = no RoPE)
+    int32_t rope_rows;      // positions in each table
+    int32_t table_stride;
+    int32_t n_seqs;
+    int32_t n_tok;
+    int32_t pad;
+    int32_t slot[kMaxBatch];
+    int32_t pos0[kMaxBatch];  // first position written
+};
+
 struct GatherArgs {
     const uint16_t* kpool;
     const uint16_t* vpool;
@@ -164,6 +189,7 @@ struct BlockCopyArgs {
 int launch_table_update(const TableUpdateArgs& a, void* stream);
 int launch_decode(const DecodeArgs& a, void* stream);
 int launch_append(const AppendArgs& a, void* stream);
+int launch_qkv_append(const QkvArgs& a, void* stream);
 int launch_gather(const GatherArgs& a, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_snapshot(const SnapshotArgs& a, void* stream);

@@ -1102,6 +1102,186 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
     __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(to + dst));
 }
 
+// ---------------------------------------------------------------------------
+// Attention producer + append: one 320-thread workgroup (5 waves) per
+// (sequence, token).  A wave works on two head rows at once, one per 32-lane
+// half, each lane holding 8 dims (16 B of bf16 input, 32 B of fp32):
+//   normalized rows, pairs (2i, 2i+1) of [q heads 0..15, k heads 0..3]:
+//     wave w takes rows 4w .. 4w+3 (wave 4: the k heads), per-head RMSNorm,
+//     partial NeoX RoPE, RNE bf16;
+//   copied rows [gate heads 0..15, v heads 0..3], same split: RNE bf16.
+// The sum of squares is a tree sum inside each 32-lane half.  The RoPE
+// partner of dim p < rope_dim/2 is p + rope_dim/2: lane ^ (rope_dim/16) for
+// rope_dim >= 16, the other half of the lane's own 8 dims for rope_dim = 8.
+// Arithmetic follows the reference's order (src/engine.cpp:3497-3512,
+// :2422-2432): (x * r) * w, then x0 c - x1 s and x1 c + x0 s without
+// contraction.  Projection rows are read once and every output written once:
+// both go non-temporal.
+constexpr int kQkvWaves = 5;
+
+template <bool BF16IN>
+__device__ __forceinline__ void load_row8(const void* base, size_t off, float (&x)[8]) {
+    if constexpr (BF16IN) {
+        const u32x4 u =
+            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[2 * j] = bf16lo(u[j]);
+            x[2 * j + 1] = bf16hi(u[j]);
+        }
+    } else {
+        const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + off);
+        const u32x4 f0 = __builtin_nontemporal_load(src);
+        const u32x4 f1 = __builtin_nontemporal_load(src + 1);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[j] = __uint_as_float(f0[j]);
+            x[4 + j] = __uint_as_float(f1[j]);
+        }
+    }
+}
+
+// RNE to bf16 with v_cvt_pk_bf16_f32 (a NaN input stays a NaN)
+__device__ __forceinline__ void store_bf16x8(uint16_t* dst, const float (&y)[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; j++) w[j] = cvt_pk_bf16(y[2 * j], y[2 * j + 1]);
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(dst));
+}
+
+// yp = y of lane ^ M (M < 32: ds_swizzle, no address arithmetic)
+template <int M>
+__device__ __forceinline__ void swap_lanes8(const float (&y)[8], float (&yp)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) yp[j] = shfl_xor<M>(y[j]);
+}
+
+// sum over the 32 lanes of each wave half
+__device__ __forceinline__ float half_wave_sum(float x) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    x += dpp<kDppRowRor8>(x);
+    return sum_xor16(x);
+}
+
+template <bool BF16IN>
+__global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
+#pragma clang fp contract(off)
+    const int b = blockIdx.x;
+    const int s = b / a.n_tok;
+    const int tok = b - s * a.n_tok;
+    const int pos = a.pos0[s] + tok;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hl = lane & 31, sub = lane >> 5;  // lane in the half, which half
+    const int d0 = hl * 8;
+    const size_t row = ((size_t)s * a.n_tok + tok) * kQkvRow;
+    const size_t orow = ((size_t)s * a.n_tok + tok) * kQHeads * kHeadDim;
+    const bool kv_wave = wave == kQkvWaves - 1;  // rows 16..19: the kv heads
+    constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
+
+    // every input row of this lane is requested before anything is stored:
+    // rows 4w + 2i + sub of [q 0..15, k 0..3] (normalized) and of
+    // [gate 0..15, v 0..3] (copied)
+    float x[2][8], c[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int r = wave * 4 + i * 2 + sub;
+        const size_t xo = kv_wave ? row + kKOff + (size_t)(r - kQHeads) * kHeadDim : row + (size_t)r * 2 * kHeadDim;
+        const size_t co = kv_wave ? row + kKOff + (size_t)(kKvHeads + r - kQHeads) * kHeadDim
+                                  : row + (size_t)r * 2 * kHeadDim + kHeadDim;
+        load_row8<BF16IN>(a.qkv, xo + d0, x[i]);
+        if (kv_wave || a.gate_out) load_row8<BF16IN>(a.qkv, co + d0, c[i]);
+    }
+    const int blk = a.table[(size_t)a.slot[s] * a.table_stride + pos / kBlockTok];
+    // RoPE coefficients of this lane's 8 dims: table entries p0 .. p0+7 for
+    // rope_dim >= 16, entries 0..3 twice for rope_dim 8
+    const int half = a.rope_half;
+    const bool roped = d0 < 2 * half;
+    float cs[8], sn[8];
+    if (roped) {
+        const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
+        const float* crow = a.rope + (size_t)pos * half + p0;
+        const float* srow = a.rope + ((size_t)a.rope_rows + pos) * half + p0;
+        const float4 c0 = *reinterpret_cast<const float4*>(crow);
+        const float4 s0 = *reinterpret_cast<const float4*>(srow);
+        const float4 c1 = half >= 8 ? *reinterpret_cast<const float4*>(crow + 4) : c0;
+        const float4 s1 = half >= 8 ? *reinterpret_cast<const float4*>(srow + 4) : s0;
+        cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w;
+        cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
+        sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            cs[j] = 1.f;
+            sn[j] = 0.f;
+        }
+    }
+    const float* wrow = (kv_wave ? a.k_norm : a.q_norm) + d0;
+    const float4 w0 = *reinterpret_cast<const float4*>(wrow);
+    const float4 w1 = *reinterpret_cast<const float4*>(wrow + 4);
+    const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+
+    // copied rows: gate heads, or (wave 4) the v heads
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int r = wave * 4 + i * 2 + sub;
+        if (kv_wave) {
+            const size_t slot =
+                (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
+            store_bf16x8(a.vpool + slot, c[i]);
+        } else if (a.gate_out) {
+            store_bf16x8(a.gate_out + orow + (size_t)r * kHeadDim + d0, c[i]);
+        }
+    }
+    // normalized rows: RMSNorm, RoPE, bf16
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int r = wave * 4 + i * 2 + sub;  // 0..15 q heads, 16..19 k heads
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss += x[i][j] * x[i][j];
+        ss = half_wave_sum(ss);
+        const float rs = 1.0f / sqrtf(ss / kHeadDim + a.eps);
+        float y[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) y[j] = x[i][j] * rs * wn[j];
+        if (half >= 8) {
+            float yp[8];
+            switch (half) {  // partner lane ^ (half / 8), uniform
+                case 8: swap_lanes8<1>(y, yp); break;
+                case 16: swap_lanes8<2>(y, yp); break;
+                case 32: swap_lanes8<4>(y, yp); break;
+                case 64: swap_lanes8<8>(y, yp); break;
+                default: swap_lanes8<16>(y, yp); break;
+            }
+            if (roped) {
+                const bool low = d0 < half;
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    y[j] = low ? y[j] * cs[j] - yp[j] * sn[j] : y[j] * cs[j] + yp[j] * sn[j];
+            }
+        } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
+            float z[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                z[j] = y[j] * cs[j] - y[j + 4] * sn[j];
+                z[j + 4] = y[j + 4] * cs[j + 4] + y[j] * sn[j + 4];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[j] = z[j];
+        }
+        if (kv_wave) {
+            const size_t slot =
+                (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
+            store_bf16x8(a.kpool + slot, y);
+        } else if (a.q_out) {
+            store_bf16x8(a.q_out + orow + (size_t)r * kHeadDim + d0, y);
+        }
+    }
+}
+
 // Gather: work item = (sequence, 32 consecutive output tokens), split over 8
 // workgroups = (K or V) x (8-token quarter); output rows are [tok][kv_head][d]
 // packed back to back.  A workgroup moves 16 KiB: each thread 4 x 16 B, all
@@ -1265,6 +1445,16 @@ int launch_prefill(const PrefillArgs& a, void* stream) {
 int launch_append(const AppendArgs& a, void* stream) {
     static_assert(2 * kKvHeads * kHeadDim * 2 / 16 == 256, "one 16-B piece per thread of a 256-thread workgroup");
     hipLaunchKernelGGL(append_kernel, dim3(a.n_seqs * a.n_tok), dim3(256), 0, (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+
+int launch_qkv_append(const QkvArgs& a, void* stream) {
+    static_assert(kQkvWaves * 4 == kQHeads + kKvHeads, "two pairs of head rows per wave");
+    const dim3 grid(a.n_seqs * a.n_tok), block(kQkvWaves * 64);
+    if (a.in_bf16)
+        hipLaunchKernelGGL(qkv_append_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(qkv_append_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 

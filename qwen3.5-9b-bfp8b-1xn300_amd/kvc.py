@@ -41,7 +41,7 @@ EXPORTS = [
     "kvc_config_default", "kvc_create", "kvc_destroy", "kvc_last_error",
     "kvc_get_stats", "kvc_abi_version", "kvc_seq_create", "kvc_seq_release",
     "kvc_seq_reset", "kvc_seq_len", "kvc_seq_truncate", "kvc_seq_reserve",
-    "kvc_seq_commit", "kvc_prefix_match", "kvc_append", "kvc_decode_attn",
+    "kvc_seq_commit", "kvc_prefix_match", "kvc_append", "kvc_qkv_append", "kvc_decode_attn",
     "kvc_prefill_attn", "kvc_gather", "kvc_state_ptrs", "kvc_snapshot_save",
     "kvc_snapshot_restore", "kvc_snapshot_release", "kvc_pool_fill_normal",
     "kvc_fill_normal_bf16", "kvc_sync",
@@ -67,6 +67,8 @@ class Config(ctypes.Structure):
         ("snapshot_slots", ctypes.c_int32), ("decode_chunk_blocks", ctypes.c_int32),
         ("device", ctypes.c_int32), ("flags", ctypes.c_uint32),
         ("alloc_seed", ctypes.c_uint64),
+        ("rms_norm_eps", ctypes.c_float), ("rope_freq_base", ctypes.c_float),
+        ("rope_dim", ctypes.c_int32), ("reserved", ctypes.c_int32),
     ]
 
 
@@ -108,6 +110,7 @@ def lib() -> ctypes.CDLL:
             "kvc_seq_commit": (ctypes.c_int, [P, pI32, I32, I32, pI32, P]),
             "kvc_prefix_match": (ctypes.c_int, [P, I32, pI32, I32, pI32, P]),
             "kvc_append": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P]),
+            "kvc_qkv_append": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, P, P]),
             "kvc_decode_attn": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
             "kvc_prefill_attn": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P, I32, F32, P]),
             "kvc_gather": (ctypes.c_int, [P, I32, pI32, I32, I32, pI32, P, P, P]),
@@ -360,6 +363,12 @@ class Context:
 
     def append(self, layer, seqs, n_tok, k, v, stream=None):
         _check(self.L.kvc_append(self.ptr, layer, _i32(seqs), len(seqs), n_tok, self._p(k), self._p(v), stream))
+
+    def qkv_append(self, layer, seqs, n_tok, qkv, q_norm, k_norm, q_out=None, gate_out=None,
+                   in_dtype=DTYPE_BF16, stream=None):
+        _check(self.L.kvc_qkv_append(self.ptr, layer, _i32(seqs), len(seqs), n_tok, self._p(qkv), in_dtype,
+                                     self._p(q_norm), self._p(k_norm), self._p(q_out), self._p(gate_out),
+                                     stream))
 
     def decode_attn(self, layer, seqs, q, out, k_new=None, v_new=None, gate=None,
                     out_dtype=DTYPE_F32, scale=1.0 / 16, stream=None):

@@ -60,6 +60,10 @@ def L() -> ctypes.CDLL:
             "orc_reuse_len": (I, [I, I, I, I, P, I, I]),
             "orc_conv_push": (None, [P, I, I, P]),
             "orc_deltanet_head_step": (None, [P, I, I, P, P, P, F, F, F, P]),
+            "orc_rope_tables": (None, [I, I, F, P, P]),
+            "orc_rms_norm_head": (None, [P, I, P, F]),
+            "orc_rope_head": (None, [P, I, P, P]),
+            "orc_qkv_produce": (None, [P, I, I, I, I, P, P, F, P, P, P, P, P, P]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(lib, n)
@@ -124,6 +128,52 @@ def decode_attn_batch(q, kcs, vcs, Ls, n_q=16, n_kv=4, d=256, scale=1 / 16, thre
     L().orc_decode_attn_batch(n, _p(q), ctypes.cast(kp, ctypes.c_void_p), ctypes.cast(vp, ctypes.c_void_p),
                               ctypes.cast(Larr, ctypes.c_void_p), n_q, n_kv, d, scale, _p(out), threads)
     return out
+
+
+# ---- K producer (RMSNorm + partial RoPE) -----------------------------------
+
+ROPE_DIM, ROPE_BASE, RMS_EPS = 64, 1.0e7, 1.0e-6  # src/model_config.h:18, :21-22
+
+
+def rope_tables(max_ctx, rope_dim=ROPE_DIM, base=ROPE_BASE):
+    half = rope_dim // 2
+    c = np.empty((max_ctx, half), np.float32)
+    s_ = np.empty((max_ctx, half), np.float32)
+    L().orc_rope_tables(max_ctx, rope_dim, base, _p(c), _p(s_))
+    return c, s_
+
+
+def rms_norm_head(x, w, eps=RMS_EPS):
+    x = np.array(x, dtype=np.float32, copy=True)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    L().orc_rms_norm_head(_p(x), x.size, _p(w), eps)
+    return x
+
+
+def rope_head(x, cos_row, sin_row, rope_dim=ROPE_DIM):
+    x = np.array(x, dtype=np.float32, copy=True)
+    c = np.ascontiguousarray(cos_row, dtype=np.float32)
+    s_ = np.ascontiguousarray(sin_row, dtype=np.float32)
+    L().orc_rope_head(_p(x), rope_dim, _p(c), _p(s_))
+    return x
+
+
+def qkv_produce(qkv_row, q_norm, k_norm, cos_row, sin_row, n_q=16, n_kv=4, d=256, rope_dim=ROPE_DIM,
+                eps=RMS_EPS):
+    """fp32 (q, gate, k, v) of one token from its projection row (fp32)."""
+    row = np.ascontiguousarray(qkv_row, dtype=np.float32)
+    assert row.size == n_q * 2 * d + 2 * n_kv * d
+    qn = np.ascontiguousarray(q_norm, dtype=np.float32)
+    kn = np.ascontiguousarray(k_norm, dtype=np.float32)
+    c = np.ascontiguousarray(cos_row, dtype=np.float32)
+    s_ = np.ascontiguousarray(sin_row, dtype=np.float32)
+    q = np.empty((n_q, d), np.float32)
+    g = np.empty((n_q, d), np.float32)
+    k = np.empty((n_kv, d), np.float32)
+    v = np.empty((n_kv, d), np.float32)
+    L().orc_qkv_produce(_p(row), n_q, n_kv, d, rope_dim, _p(qn), _p(kn), eps, _p(c), _p(s_),
+                        _p(q), _p(g), _p(k), _p(v))
+    return q, g, k, v
 
 
 def reference_prefix(cached, prompt):

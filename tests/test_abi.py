@@ -29,7 +29,7 @@ def test_exports_match_header():
     lib = kvc.lib()
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.kvc_abi_version() == 1
+    assert lib.kvc_abi_version() == 2
 
 
 def test_config_default_and_struct_layout():
@@ -37,7 +37,8 @@ def test_config_default_and_struct_layout():
     assert (cfg.n_attn_layers, cfg.n_ssm_layers, cfg.n_q_heads, cfg.n_kv_heads, cfg.head_dim) == (8, 24, 16, 4, 256)
     assert (cfg.block_tokens, cfg.snapshot_interval) == (32, 256)
     assert (cfg.ssm_v_heads, cfg.ssm_k_dim, cfg.ssm_v_dim, cfg.conv_rows, cfg.conv_channels) == (32, 128, 128, 3, 8192)
-    assert ctypes.sizeof(kvc.Config) == 96
+    assert (cfg.rope_dim, cfg.rope_freq_base, cfg.rms_norm_eps) == (64, 1.0e7, np.float32(1e-6))
+    assert ctypes.sizeof(kvc.Config) == 112
 
 
 def test_unsupported_shapes_rejected():
@@ -53,6 +54,14 @@ def test_unsupported_shapes_rejected():
     with pytest.raises(kvc.KvcError) as e:
         host_ctx(flags=kvc.FLAG_DECODE_SPLIT_D | kvc.FLAG_DECODE_NO_SPLIT_D)
     assert e.value.code == kvc.KVC_ERR_INVALID
+    for rd in (4, 48, 512):
+        with pytest.raises(kvc.KvcError) as e:
+            host_ctx(rope_dim=rd)
+        assert e.value.code == kvc.KVC_ERR_UNSUPPORTED
+    with pytest.raises(kvc.KvcError) as e:
+        host_ctx(rope_freq_base=0.0)
+    assert e.value.code == kvc.KVC_ERR_INVALID
+    host_ctx(rope_dim=0).close()  # RoPE off is a valid model
 
 
 def test_device_ops_fail_loudly_on_host_only_context():
@@ -64,6 +73,9 @@ def test_device_ops_fail_loudly_on_host_only_context():
         assert e.value.code == kvc.KVC_ERR_NO_DEVICE
         with pytest.raises(kvc.KvcError) as e:
             c.append(0, [s], 1, 1, 1)
+        assert e.value.code == kvc.KVC_ERR_NO_DEVICE
+        with pytest.raises(kvc.KvcError) as e:
+            c.qkv_append(0, [s], 1, 1, 1, 1)
         assert e.value.code == kvc.KVC_ERR_NO_DEVICE
 
 
