@@ -42,6 +42,7 @@ HBM_PEAK_GBS = 8000.0
 NQ, NKV, D, BT = 16, 4, 256, 32
 ROW = NKV * D
 SEED = 20261201
+O_SSM_PROJ = 8192 + 4096 + 2 * 32  # Gated-DeltaNet projection row: conv inputs, z, alpha, beta
 METRIC = "KV path HBM GB/s (% of 8 TB/s) + µs/layer decode attn at 4K ctx, 1 GPU"
 
 
@@ -511,11 +512,61 @@ def run_e(args):
     per_sess = state_bytes + 8 * 2 * iv * ROW * 2
     moved = 2 * per_sess * nses  # read + write
     sv_ms, rs_ms = sv / reps, rs / reps
+
+    # resume: restore the 64 sessions, then run the 24 Gated-DeltaNet layers
+    # on the GPU in place on the restored state -- one decode token, and one
+    # 128-token chunk (state kept in registers across the chunk).  Each leg is
+    # one HIP graph of its 24 layer launches, replayed between two events.
+    ids = ctx.snapshot_save(src, stream)
+    ctx.snapshot_restore(dst, ids, stream)
+    for i in ids:
+        ctx.snapshot_release(i)
+    n_chunk, proj_row, out_row = 128, O_SSM_PROJ, cf.ssm_v_heads * cf.ssm_v_dim
+    rng = np.random.default_rng(SEED + 51)
+    wts = [kvc.to_device(x_) for x_ in (
+        (0.5 * rng.standard_normal((4, cf.conv_channels))).astype(np.float32),
+        rng.standard_normal(cf.ssm_v_heads).astype(np.float32),
+        -rng.uniform(0.05, 1.0, cf.ssm_v_heads).astype(np.float32),
+        rng.uniform(0.5, 1.5, cf.ssm_v_dim).astype(np.float32))]
+    proj = h.malloc(nses * n_chunk * proj_row * 2)
+    ctx.fill_normal_bf16(proj, nses * n_chunk * proj_row, SEED + 52, 1.0, stream)
+    dn_out = h.malloc(nses * n_chunk * out_row * 2)
+    n_ssm = cf.n_ssm_layers
+
+    def dn_leg(n_tok):
+        return lambda: [ctx.deltanet_step(l_, dst, n_tok, proj, wts[0], wts[1], wts[2], wts[3], dn_out,
+                                          in_dtype=kvc.DTYPE_BF16, out_dtype=kvc.DTYPE_BF16, stream=stream)
+                        for l_ in range(n_ssm)]
+
+    dn_us = {}
+    for name, n_tok, n_rep in (("decode", 1, 20), ("chunk", n_chunk, 2)):
+        g_ = h.capture(stream, dn_leg(n_tok))
+        h.graph_launch(g_, stream)  # warm-up
+        h.record(e0, stream)
+        for _ in range(n_rep):
+            h.graph_launch(g_, stream)
+        h.record(e1, stream)
+        dn_us[name] = h.elapsed_ms(e0, e1) * 1e3 / (n_rep * n_ssm)
+        h.graph_destroy(g_)
+    layer_state = rec_b + conv_b
+    dec_bytes = nses * (2 * layer_state + proj_row * 2 + out_row * 2)
+    chunk_bytes = nses * (2 * layer_state + n_chunk * (proj_row * 2 + out_row * 2))
+    # delta rule per token and layer: 32 v-heads x 128 x 128 state x (decay mul + 3 FMA)
+    chunk_flops = nses * n_chunk * cf.ssm_v_heads * cf.ssm_v_dim * cf.ssm_k_dim * 7
+    for b_ in wts + [proj, dn_out]:
+        b_.free()
     ctx.close()
     return {"workload": "e: 24 Gated-DeltaNet + 8 attention layers, 64 sessions, save then restore at a 256-token "
-                        "boundary (fp32 recurrent + conv state, bf16 K/V of the segment)",
+                        "boundary (fp32 recurrent + conv state, bf16 K/V of the segment), then resume: the 24 "
+                        "Gated-DeltaNet layers on the restored state for one decode token and for a 128-token "
+                        "chunk (bf16 projection rows in, bf16 out)",
             "bytes_per_session": per_sess, "save_ms": round(sv_ms, 3), "restore_ms": round(rs_ms, 3),
             "save_GBps": round(moved / (sv_ms * 1e-3) / 1e9, 1), "restore_GBps": round(moved / (rs_ms * 1e-3) / 1e9, 1),
+            "resume_decode_us_per_layer": round(dn_us["decode"], 1),
+            "resume_decode_GBps": round(dec_bytes / (dn_us["decode"] * 1e-6) / 1e9, 1),
+            "resume_chunk128_us_per_layer": round(dn_us["chunk"], 1),
+            "resume_chunk128_GBps": round(chunk_bytes / (dn_us["chunk"] * 1e-6) / 1e9, 1),
+            "resume_chunk128_TFLOPs": round(chunk_flops / (dn_us["chunk"] * 1e-6) / 1e12, 2),
             "hbm_context_bytes": int(st.hbm_bytes)}
 
 

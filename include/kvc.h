@@ -22,6 +22,9 @@
  *   kvc_gather                  reads the cache in the reference layout
  *                               [pos][kv_head][d], src/engine.cpp:3539
  *   kvc_state_ptrs              g_ssm_state / g_conv_state, src/engine.cpp:86-94
+ *   kvc_deltanet_step           the Gated-DeltaNet layer step that mutates that
+ *                               state (conv1d + delta rule + gated RMSNorm),
+ *                               src/engine.cpp:3197-3327 and :2600-2716
  *   kvc_snapshot_save/_restore  prefix-boundary copies of that state (new: the
  *                               reference can only extend one live sequence)
  *
@@ -211,6 +214,24 @@ int kvc_gather(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
  * [v_heads][v_dim][k_dim], conv = fp32 [conv_rows][conv_channels]. */
 int kvc_state_ptrs(kvc_ctx* ctx, int32_t seq, int32_t ssm_layer, void** rec,
                    void** conv);
+/* Gated-DeltaNet step of n_tok tokens per seq, in place on the state above
+ * (src/engine.cpp:3197-3327 decode, :2600-2716 prefill, token by token).
+ * proj: [n_seqs][n_tok][row], row = conv_channels raw inputs (q | k | v) +
+ * v_heads*v_dim z + v_heads alpha + v_heads beta (12352 at the Qwen3.5
+ * shapes), fp32 or bf16 by in_dtype.  Device fp32 weights: conv_w
+ * [conv_rows + 1][conv_channels] tap-major (taps 0..2 on the window, oldest
+ * first, tap 3 on the input), dt_bias [v_heads], a [v_heads] (decay =
+ * exp(softplus(alpha + dt_bias) * a)), norm_w [v_dim].  out: [n_seqs][n_tok]
+ * [v_heads * v_dim], fp32 or bf16 (RNE) by out_dtype: the gated-RMSNorm
+ * output (o / rms(o) * norm_w * silu(z), o = S q / 11.3137).  exp, sigmoid and
+ * SiLU are exact where the reference uses Schraudolph approximations
+ * (:2349-2374).  Built for 32 v-heads, 16 k-heads, 128 x 128 heads, a 3-row
+ * window and 8192 channels (KVC_ERR_UNSUPPORTED otherwise). */
+int kvc_deltanet_step(kvc_ctx* ctx, int32_t ssm_layer, const int32_t* seqs,
+                      int32_t n_seqs, int32_t n_tok, const void* proj,
+                      int32_t in_dtype, const void* conv_w, const void* dt_bias,
+                      const void* a, const void* norm_w, void* out,
+                      int32_t out_dtype, void* stream);
 /* Save each seq's state and the K/V of its last snapshot_interval tokens (all
  * attention layers).  Each seq length must be a positive multiple of
  * snapshot_interval.  snap_ids receives one id per seq.  Bit-exact copies. */

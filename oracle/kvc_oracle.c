@@ -39,6 +39,12 @@
  *                        (sign and pairing); pair norms preserved; dims >=
  *                        rope_dim untouched; rotating by positions a then b
  *                        equals a + b to fp32 accuracy
+ *   deltanet_layer_step  composition of the pinned conv_push and
+ *                        deltanet_head_step; delta-rule invariant S'k = v
+ *                        for beta -> 1, a = 0 (decay 1); decay = e^(softplus
+ *                        * a) at chosen alpha; a zero projection row leaves
+ *                        the state scaled by the decay and gives zero output;
+ *                        gated norm: output RMS = |norm_w| for silu(z) = z
  *   qkv_produce          deinterleave: gate rows and v rows are copies of
  *                        the input rows; q/k equal norm-then-rope of their
  *                        rows (composition of the two pinned steps)
@@ -415,5 +421,65 @@ void orc_qkv_produce(const float* qkv, int n_q, int n_kv, int d, int rope_dim,
             if (rope_dim > 0) orc_rope_head(kh, rope_dim, cos_row, sin_row);
         }
         if (v) memcpy(v + (size_t)h * d, vrow + (size_t)h * d, sizeof(float) * d);
+    }
+}
+
+/* ---------------------------------------------------------------------- */
+/* Gated-DeltaNet layer step                                                */
+
+static float orc_silu(float x, int fast) { return x * orc_sigmoid(x, fast); }
+
+void orc_deltanet_layer_step(float* conv_state, float* ssm_state, const float* proj,
+                             const float* conv_w, const float* dt_bias, const float* a,
+                             const float* norm_w, int n_v, int n_k, int dk, int dv,
+                             float eps, float out_scale, int fast, float* out) {
+    const int C = 2 * n_k * dk + n_v * dv;
+    const float* x = proj;
+    const float* z = proj + C;
+    const float* alpha = z + (size_t)n_v * dv;
+    const float* beta_raw = alpha + n_v;
+    float conv[16384];
+    if (C > 16384 || dk > 512 || dv > 512) return;
+    const float* s0 = conv_state;
+    const float* s1 = conv_state + C;
+    const float* s2 = conv_state + 2 * (size_t)C;
+    for (int ch = 0; ch < C; ch++) { /* :3209-3226 */
+        float sum = s0[ch] * conv_w[ch];
+        sum = fmaf(s1[ch], conv_w[C + ch], sum);
+        sum = fmaf(s2[ch], conv_w[2 * (size_t)C + ch], sum);
+        sum = fmaf(x[ch], conv_w[3 * (size_t)C + ch], sum);
+        conv[ch] = orc_silu(sum, fast);
+    }
+    orc_conv_push(conv_state, 3, C, x); /* :3228-3230 */
+    const float* cq = conv;
+    const float* ck = conv + (size_t)n_k * dk;
+    const float* cv = conv + 2 * (size_t)n_k * dk;
+    for (int vh = 0; vh < n_v; vh++) {
+        const int kh = vh % n_k;
+        float q[512], k[512], o[512];
+        float qn = 0.0f, kn = 0.0f;
+        for (int j = 0; j < dk; j++) {
+            q[j] = cq[(size_t)kh * dk + j];
+            k[j] = ck[(size_t)kh * dk + j];
+            qn = fmaf(q[j], q[j], qn);
+            kn = fmaf(k[j], k[j], kn);
+        }
+        const float qs = 1.0f / sqrtf(qn + eps), ks = 1.0f / sqrtf(kn + eps);
+        for (int j = 0; j < dk; j++) {
+            q[j] *= qs;
+            k[j] *= ks;
+        }
+        const float biased = alpha[vh] + dt_bias[vh];
+        const float ex = fast ? orc_fast_expf(biased) : expf(biased);
+        const float sp = biased > 20.0f ? biased : logf(1.0f + ex);
+        const float decay = expf(sp * a[vh]);
+        const float beta = orc_sigmoid(beta_raw[vh], fast);
+        orc_deltanet_head_step(ssm_state + (size_t)vh * dv * dk, dv, dk, q, k, cv + (size_t)vh * dv, decay,
+                               beta, out_scale, o);
+        float ss = 0.0f;
+        for (int i = 0; i < dv; i++) ss = fmaf(o[i], o[i], ss);
+        const float rms = 1.0f / sqrtf(ss / dv + eps);
+        for (int i = 0; i < dv; i++)
+            out[(size_t)vh * dv + i] = o[i] * rms * norm_w[i] * orc_silu(z[(size_t)vh * dv + i], fast);
     }
 }

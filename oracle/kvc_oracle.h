@@ -124,6 +124,26 @@ void orc_deltanet_head_step(float* state, int dv, int dk, const float* q,
                             const float* k, const float* v, float decay,
                             float beta, float out_scale, float* out);
 
+/* One Gated-DeltaNet layer for one token, in place on conv_state [3][C] and
+ * ssm_state [n_v][dv][dk], src/engine.cpp:3197-3327 (decode) and :2600-2716
+ * (prefill, per token).  proj = [C conv inputs (q n_k*dk | k n_k*dk | v
+ * n_v*dv)][n_v*dv z][n_v alpha][n_v beta], C = 2*n_k*dk + n_v*dv.
+ *   conv:  c = silu(s0 w0 + s1 w1 + s2 w2 + x w3) with w [4][C] tap-major,
+ *          then the window push (:3204-3232)
+ *   q, k of k-head vh % n_k: x / sqrtf(sum x^2 + eps) (:3261-3275)
+ *   decay = exp(softplus(alpha + dt_bias) * a), beta = sigmoid(beta_raw)
+ *          with softplus(b) = b for b > 20 (:3277-3281)
+ *   delta rule per v-head row i: S_i *= decay; S_i += k beta (v_i - S_i.k);
+ *          o_i = (S_i.q) * out_scale (:3283-3305)
+ *   gated RMSNorm: out = o / sqrtf(mean(o^2) + eps) * norm_w * silu(z)
+ *          (:3308-3320)
+ * fast = 1 uses the reference's Schraudolph exp in softplus, sigmoid and SiLU
+ * (:2349-2374); fast = 0 uses libm expf (the HIP path's semantics). */
+void orc_deltanet_layer_step(float* conv_state, float* ssm_state, const float* proj,
+                             const float* conv_w, const float* dt_bias, const float* a,
+                             const float* norm_w, int n_v, int n_k, int dk, int dv,
+                             float eps, float out_scale, int fast, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1184,6 +1184,52 @@ int kvc_state_ptrs(kvc_ctx* c, int32_t seq, int32_t ssm_layer, void** rec, void*
     return KVC_OK;
 }
 
+int kvc_deltanet_step(kvc_ctx* c, int32_t ssm_layer, const int32_t* seqs, int32_t n_seqs, int32_t n_tok,
+                      const void* proj, int32_t in_dtype, const void* conv_w, const void* dt_bias, const void* a,
+                      const void* norm_w, void* out, int32_t out_dtype, void* stream) {
+    if (!c) return set_err(KVC_ERR_INVALID, "null context");
+    int rc;
+    if ((rc = check_device(c)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
+    const kvc_config& k = c->cfg;
+    if (ssm_layer < 0 || ssm_layer >= k.n_ssm_layers)
+        return set_err(KVC_ERR_RANGE, "ssm_layer %d out of range [0, %d)", ssm_layer, k.n_ssm_layers);
+    if (k.ssm_v_heads != kSsmVHeads || k.ssm_k_dim != kSsmDk || k.ssm_v_dim != kSsmDv ||
+        k.conv_rows != kSsmConvRows || k.conv_channels != kSsmC)
+        return set_err(KVC_ERR_UNSUPPORTED,
+                       "the DeltaNet step is built for %d v-heads, %dx%d heads, %d conv rows, %d channels",
+                       kSsmVHeads, kSsmDv, kSsmDk, kSsmConvRows, kSsmC);
+    if (!proj || !conv_w || !dt_bias || !a || !norm_w || !out || n_tok <= 0)
+        return set_err(KVC_ERR_INVALID, "deltanet step needs proj, weights, out and n_tok > 0");
+    if ((in_dtype != KVC_DTYPE_F32 && in_dtype != KVC_DTYPE_BF16) ||
+        (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16))
+        return set_err(KVC_ERR_INVALID, "bad in_dtype / out_dtype");
+    const size_t isz = in_dtype == KVC_DTYPE_BF16 ? 2 : 4, osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
+    for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+        const int32_t n = std::min(kMaxBatch, n_seqs - i0);
+        DeltaNetArgs d{};
+        d.proj = static_cast<const uint8_t*>(proj) + (size_t)i0 * n_tok * kSsmProj * isz;
+        d.conv_w = static_cast<const float*>(conv_w);
+        d.dt_bias = static_cast<const float*>(dt_bias);
+        d.a = static_cast<const float*>(a);
+        d.norm_w = static_cast<const float*>(norm_w);
+        d.out = static_cast<uint8_t*>(out) + (size_t)i0 * n_tok * kSsmVHeads * kSsmDv * osz;
+        d.state = c->d_state;
+        d.state_bytes = c->state_bytes;
+        d.layer_off = (int64_t)ssm_layer * (c->rec_bytes + c->conv_bytes);
+        d.rec_bytes = c->rec_bytes;
+        d.eps = k.rms_norm_eps;
+        d.out_scale = 1.0f / 11.3137f;  // src/engine.cpp:3251
+        d.in_bf16 = in_dtype == KVC_DTYPE_BF16;
+        d.out_bf16 = out_dtype == KVC_DTYPE_BF16;
+        d.n_seqs = n;
+        d.n_tok = n_tok;
+        for (int32_t j = 0; j < n; j++) d.slot[j] = seqs[i0 + j];
+        int e = launch_deltanet(d, stream);
+        if (e) return hip_err((hipError_t)e, "deltanet launch");
+    }
+    return KVC_OK;
+}
+
 int kvc_snapshot_save(kvc_ctx* c, const int32_t* seqs, int32_t n_seqs, int32_t* snap_ids, void* stream) {
     if (!c || !snap_ids) return set_err(KVC_ERR_INVALID, "null argument");
     int rc;

@@ -116,6 +116,35 @@ struct QkvArgs {
     int32_t pos0[kMaxBatch];  // first position written
 };
 
+// Gated-DeltaNet shapes the step kernel is built for (model_config.h:25-31)
+constexpr int kSsmVHeads = 32;
+constexpr int kSsmKHeads = 16;
+constexpr int kSsmDk = 128;
+constexpr int kSsmDv = 128;
+constexpr int kSsmConvRows = 3;
+constexpr int kSsmC = 2 * kSsmKHeads * kSsmDk + kSsmVHeads * kSsmDv;  // 8192 conv channels
+constexpr int kSsmProj = kSsmC + kSsmVHeads * kSsmDv + 2 * kSsmVHeads;  // 12352 per token
+
+struct DeltaNetArgs {
+    const void* proj;       // [n_seqs][n_tok][kSsmProj], fp32 or bf16
+    const float* conv_w;    // [4][kSsmC] tap-major
+    const float* dt_bias;   // [kSsmVHeads]
+    const float* a;         // [kSsmVHeads]
+    const float* norm_w;    // [kSsmDv]
+    void* out;              // [n_seqs][n_tok][kSsmVHeads * kSsmDv]
+    uint8_t* state;         // state pool base
+    int64_t state_bytes;    // per sequence slot
+    int64_t layer_off;      // byte offset of this layer's rec state inside a slot
+    int64_t rec_bytes;      // conv state follows the rec state
+    float eps;
+    float out_scale;
+    int32_t in_bf16;
+    int32_t out_bf16;
+    int32_t n_seqs;
+    int32_t n_tok;
+    int32_t slot[kMaxBatch];
+};
+
 struct GatherArgs {
     const uint16_t* kpool;
     const uint16_t* vpool;
@@ -190,6 +219,7 @@ int launch_table_update(const TableUpdateArgs& a, void* stream);
 int launch_decode(const DecodeArgs& a, void* stream);
 int launch_append(const AppendArgs& a, void* stream);
 int launch_qkv_append(const QkvArgs& a, void* stream);
+int launch_deltanet(const DeltaNetArgs& a, void* stream);
 int launch_gather(const GatherArgs& a, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_snapshot(const SnapshotArgs& a, void* stream);

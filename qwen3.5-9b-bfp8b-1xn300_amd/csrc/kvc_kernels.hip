@@ -1282,6 +1282,298 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Gated-DeltaNet step (src/engine.cpp:3197-3327 decode, :2600-2716 prefill),
+// in place on the library's recurrent state [32][128 v][128 k] and conv window
+// [3][8192] of one layer.  Workgroup = (sequence, k-head kh): it owns the q and
+// k channels of kh and the v channels of the two v-heads kh and kh + 16 that
+// read them (v-head vh uses k-head vh % 16), so every conv channel and every
+// state row has exactly one owner and the whole step is one launch.
+//   state rows: wave w takes v-head kh + 16 (w / 4) and rows
+//     32 (w % 4) + 4 r + lane / 16 (r = 0..7); lane l holds k-columns
+//     4c .. 4c+3 and 64+4c .. 64+4c+3 (c = l % 16) of its rows, so each 16-B
+//     access of a row group is one contiguous 256-B run and a row's dot
+//     products reduce over one 16-lane DPP row (4 steps, no cross-row
+//     traffic);
+//   conv: thread t owns channel t of [q_kh | k_kh | v_vh0 | v_vh1] with its
+//     3-row window in registers.
+// Per token: conv + SiLU -> LDS, barrier; q, k L2-normalised; decay and beta;
+// the delta rule row by row (S *= decay; S += k beta (v_i - S.k); o_i = S.q *
+// scale); barrier; gated RMSNorm with SiLU(z).  exp, sigmoid and SiLU are
+// exact where the reference uses Schraudolph approximations
+// (src/engine.cpp:2349-2374).  Two kernels share the row arithmetic (dn_row),
+// so a token gives the same bits through either: deltanet_kernel keeps both
+// state slabs in registers across a chunk of tokens; deltanet_decode_kernel
+// (one token) streams the rows -- loaded ahead, stored as soon as updated.
+constexpr int kDnThreads = 512;
+constexpr int kDnCols = 8;   // k-columns per lane (16 lanes per state row)
+constexpr int kDnRows = 8;   // state rows per lane
+
+template <bool BF16IN>
+__device__ __forceinline__ float load_f(const void* base, size_t off) {
+    if constexpr (BF16IN)
+        return bf16f(static_cast<const uint16_t*>(base)[off]);
+    else
+        return static_cast<const float*>(base)[off];
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
+
+// sum over the 16 lanes of a DPP row (every lane gets the sum)
+__device__ __forceinline__ float sum16(float x) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    x += dpp<kDppHalfMirror>(x);  // quads uniform: pairs quad 0 with quad 1
+    return x + dpp<kDppRowRor8>(x);
+}
+
+// One state row (this lane's 8 columns): decay, delta-rule update; returns
+// the row's output dot S_i.q (before the scale).
+__device__ __forceinline__ float dn_row(float (&st)[kDnCols], const float (&k)[kDnCols], const float (&q)[kDnCols],
+                                        float decay, float beta, float vi) {
+#pragma clang fp contract(off)
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < kDnCols; j += 2) {
+        st[j] *= decay;
+        st[j + 1] *= decay;
+        s0 = fmaf(st[j], k[j], s0);
+        s1 = fmaf(st[j + 1], k[j + 1], s1);
+    }
+    const float sk = sum16(s0 + s1);
+    const float dd = beta * (vi - sk);
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < kDnCols; j += 2) {
+        st[j] = fmaf(k[j], dd, st[j]);
+        st[j + 1] = fmaf(k[j + 1], dd, st[j + 1]);
+        o0 = fmaf(st[j], q[j], o0);
+        o1 = fmaf(st[j + 1], q[j + 1], o1);
+    }
+    return sum16(o0 + o1);
+}
+
+// Shared per-token front end: this lane's normalised q and k columns, decay
+// and beta of the wave's v-head (conv_lds holds the token's SiLU'd conv).
+__device__ __forceinline__ void dn_qk(const float* conv_lds, int col0, float eps, float (&q)[kDnCols],
+                                      float (&k)[kDnCols]) {
+#pragma clang fp contract(off)
+    float qn = 0.f, kn = 0.f;
+#pragma unroll
+    for (int j = 0; j < kDnCols; j += 4) {
+        const int c = col0 + (j ? kSsmDk / 2 : 0);  // columns 4c.. and 64+4c..
+        const float4 qq = *reinterpret_cast<const float4*>(conv_lds + c);
+        const float4 kk = *reinterpret_cast<const float4*>(conv_lds + 128 + c);
+        q[j] = qq.x; q[j + 1] = qq.y; q[j + 2] = qq.z; q[j + 3] = qq.w;
+        k[j] = kk.x; k[j + 1] = kk.y; k[j + 2] = kk.z; k[j + 3] = kk.w;
+    }
+#pragma unroll
+    for (int j = 0; j < kDnCols; j++) {
+        qn = fmaf(q[j], q[j], qn);
+        kn = fmaf(k[j], k[j], kn);
+    }
+    qn = sum16(qn);
+    kn = sum16(kn);
+    const float qs = 1.0f / sqrtf(qn + eps), ks = 1.0f / sqrtf(kn + eps);
+#pragma unroll
+    for (int j = 0; j < kDnCols; j++) {
+        q[j] *= qs;
+        k[j] *= ks;
+    }
+}
+
+__device__ __forceinline__ void dn_gates(float alpha, float braw, float dtb, float av, float& decay, float& beta) {
+#pragma clang fp contract(off)
+    const float biased = alpha + dtb;
+    const float sp = biased > 20.0f ? biased : logf(1.0f + expf(biased));
+    decay = expf(sp * av);
+    beta = sigmoid_f(braw);
+}
+
+// gated RMSNorm of one v-head's 128 outputs (o_row) and the store of dims
+// 32 wi .. +31 (lanes 0..31)
+__device__ __forceinline__ void dn_norm_out(const DeltaNetArgs& a, const float* o_row, int lane, int wi, int vh,
+                                            size_t out_row, float z) {
+#pragma clang fp contract(off)
+    const float o0 = o_row[lane], o1 = o_row[lane + 64];
+    const float ss = wave_sum(fmaf(o0, o0, o1 * o1));
+    const float rms = 1.0f / sqrtf(ss / kSsmDv + a.eps);
+    if (lane < 32) {
+        const int d = wi * 32 + lane;
+        const float y = o_row[d] * rms * a.norm_w[d] * silu_f(z);
+        const size_t oi = out_row + (size_t)vh * kSsmDv + d;
+        if (a.out_bf16)
+            static_cast<uint16_t*>(a.out)[oi] = (uint16_t)f32_to_bf16_rne(y);
+        else
+            static_cast<float*>(a.out)[oi] = y;
+    }
+}
+
+__device__ __forceinline__ int dn_channel(int t, int kh) {
+    const int part = t >> 7, ci = t & 127;
+    return part == 0   ? kh * kSsmDk + ci
+           : part == 1 ? kSsmKHeads * kSsmDk + kh * kSsmDk + ci
+                       : 2 * kSsmKHeads * kSsmDk + (kh + kSsmKHeads * (part - 2)) * kSsmDv + ci;
+}
+
+template <bool BF16IN>
+__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void deltanet_kernel(DeltaNetArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float conv_lds[4 * 128];  // q_kh, k_kh, v_vh0, v_vh1 (SiLU'd conv outputs)
+    __shared__ float o_lds[2][kSsmDv];   // scaled recurrence outputs of the two v-heads
+    __shared__ float4 cw_lds[kDnThreads];  // conv taps of each owned channel
+    __shared__ float4 win_lds[kDnThreads];  // conv window of each owned channel (w = unused)
+    const int b = blockIdx.x;
+    const int s = b / kSsmKHeads;
+    const int kh = b - s * kSsmKHeads;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: head data in SGPRs
+    const int vl = wave >> 2, wi = wave & 3;
+    const int vh = kh + kSsmKHeads * vl;
+    const int rg = lane >> 4, col0 = (lane & 15) * 4;
+    const int rbase = wi * 32 + rg;  // rows rbase + 4 r
+
+    uint8_t* slot = a.state + (size_t)a.slot[s] * a.state_bytes + a.layer_off;
+    float* S = reinterpret_cast<float*>(slot) + (size_t)vh * kSsmDv * kSsmDk + col0;
+    float* conv = reinterpret_cast<float*>(slot + a.rec_bytes);
+
+    float st[kDnRows][kDnCols];
+#pragma unroll
+    for (int r = 0; r < kDnRows; r++) {
+        const float* src = S + (size_t)(rbase + 4 * r) * kSsmDk;
+        const float4 x0 = *reinterpret_cast<const float4*>(src);
+        const float4 x1 = *reinterpret_cast<const float4*>(src + kSsmDk / 2);
+        st[r][0] = x0.x; st[r][1] = x0.y; st[r][2] = x0.z; st[r][3] = x0.w;
+        st[r][4] = x1.x; st[r][5] = x1.y; st[r][6] = x1.z; st[r][7] = x1.w;
+    }
+    const int ch = dn_channel(t, kh);
+    cw_lds[t] = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch], a.conv_w[3 * kSsmC + ch]);
+    win_lds[t] = make_float4(conv[ch], conv[kSsmC + ch], conv[2 * kSsmC + ch], 0.f);
+    const float dtb = a.dt_bias[vh], av = a.a[vh];
+    constexpr size_t kZ = kSsmC, kAlpha = kSsmC + kSsmVHeads * kSsmDv, kBeta = kAlpha + kSsmVHeads;
+    // the next token's inputs are requested while the current one computes
+    const int zd = wi * 32 + (lane & 31);  // gated-norm dim of this lane
+    const size_t prow0 = (size_t)s * a.n_tok * kSsmProj;
+    float nx = load_f<BF16IN>(a.proj, prow0 + ch);
+    float nalpha = load_f<BF16IN>(a.proj, prow0 + kAlpha + vh);
+    float nbraw = load_f<BF16IN>(a.proj, prow0 + kBeta + vh);
+    float nz = load_f<BF16IN>(a.proj, prow0 + kZ + (size_t)vh * kSsmDv + zd);
+
+    for (int tok = 0; tok < a.n_tok; tok++) {
+        const float x = nx, alpha = nalpha, braw = nbraw, z = nz;
+        if (tok + 1 < a.n_tok) {
+            const size_t nrow = prow0 + (size_t)(tok + 1) * kSsmProj;
+            nx = load_f<BF16IN>(a.proj, nrow + ch);
+            nalpha = load_f<BF16IN>(a.proj, nrow + kAlpha + vh);
+            nbraw = load_f<BF16IN>(a.proj, nrow + kBeta + vh);
+            nz = load_f<BF16IN>(a.proj, nrow + kZ + (size_t)vh * kSsmDv + zd);
+        }
+        const float4 cw = cw_lds[t];  // each thread reads only its own entries
+        const float4 win = win_lds[t];
+        float sum = win.x * cw.x;
+        sum = fmaf(win.y, cw.y, sum);
+        sum = fmaf(win.z, cw.z, sum);
+        sum = fmaf(x, cw.w, sum);
+        conv_lds[t] = silu_f(sum);
+        win_lds[t] = make_float4(win.y, win.z, x, 0.f);
+        __syncthreads();
+
+        float q[kDnCols], k[kDnCols], decay, beta;
+        dn_qk(conv_lds, col0, a.eps, q, k);
+        dn_gates(alpha, braw, dtb, av, decay, beta);
+        // the 16 lanes of a row hold the same output and all store it (one
+        // LDS word, same value): no branch between the rows
+#pragma unroll
+        for (int r = 0; r < kDnRows; r++)
+            o_lds[vl][rbase + 4 * r] =
+                dn_row(st[r], k, q, decay, beta, conv_lds[256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
+        __syncthreads();
+        dn_norm_out(a, o_lds[vl], lane, wi, vh, ((size_t)s * a.n_tok + tok) * (kSsmVHeads * kSsmDv), z);
+    }
+#pragma unroll
+    for (int r = 0; r < kDnRows; r++) {
+        float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
+        *reinterpret_cast<float4*>(dst) = make_float4(st[r][0], st[r][1], st[r][2], st[r][3]);
+        *reinterpret_cast<float4*>(dst + kSsmDk / 2) = make_float4(st[r][4], st[r][5], st[r][6], st[r][7]);
+    }
+    const float4 win = win_lds[t];
+    conv[ch] = win.x;
+    conv[kSsmC + ch] = win.y;
+    conv[2 * kSsmC + ch] = win.z;
+}
+
+constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel
+
+template <bool BF16IN>
+__global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArgs a) {
+#pragma clang fp contract(off)
+    __shared__ float conv_lds[4 * 128];
+    __shared__ float o_lds[2][kSsmDv];
+    const int b = blockIdx.x;
+    const int s = b / kSsmKHeads;
+    const int kh = b - s * kSsmKHeads;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int vl = wave >> 2, wi = wave & 3;
+    const int vh = kh + kSsmKHeads * vl;
+    const int rg = lane >> 4, col0 = (lane & 15) * 4;
+    const int rbase = wi * 32 + rg;
+
+    uint8_t* slot = a.state + (size_t)a.slot[s] * a.state_bytes + a.layer_off;
+    float* S = reinterpret_cast<float*>(slot) + (size_t)vh * kSsmDv * kSsmDk + col0;
+    float* conv = reinterpret_cast<float*>(slot + a.rec_bytes);
+
+    float4 buf[kDnPf][2];
+#pragma unroll
+    for (int p = 0; p < kDnPf; p++) {
+        const float* src = S + (size_t)(rbase + 4 * p) * kSsmDk;
+        buf[p][0] = *reinterpret_cast<const float4*>(src);
+        buf[p][1] = *reinterpret_cast<const float4*>(src + kSsmDk / 2);
+    }
+    const int ch = dn_channel(t, kh);
+    const size_t prow = (size_t)s * kSsmProj;
+    constexpr size_t kZ = kSsmC, kAlpha = kSsmC + kSsmVHeads * kSsmDv, kBeta = kAlpha + kSsmVHeads;
+    const int zd = wi * 32 + (lane & 31);
+    const float x = load_f<BF16IN>(a.proj, prow + ch);
+    const float z = load_f<BF16IN>(a.proj, prow + kZ + (size_t)vh * kSsmDv + zd);
+    const float alpha = load_f<BF16IN>(a.proj, prow + kAlpha + vh);
+    const float braw = load_f<BF16IN>(a.proj, prow + kBeta + vh);
+    const float c0 = conv[ch], c1 = conv[kSsmC + ch], c2 = conv[2 * kSsmC + ch];
+    float sum = c0 * a.conv_w[ch];
+    sum = fmaf(c1, a.conv_w[kSsmC + ch], sum);
+    sum = fmaf(c2, a.conv_w[2 * kSsmC + ch], sum);
+    sum = fmaf(x, a.conv_w[3 * kSsmC + ch], sum);
+    conv_lds[t] = silu_f(sum);
+    conv[ch] = c1;
+    conv[kSsmC + ch] = c2;
+    conv[2 * kSsmC + ch] = x;
+    __syncthreads();
+
+    float q[kDnCols], k[kDnCols], decay, beta;
+    dn_qk(conv_lds, col0, a.eps, q, k);
+    dn_gates(alpha, braw, a.dt_bias[vh], a.a[vh], decay, beta);
+#pragma unroll
+    for (int r = 0; r < kDnRows; r++) {
+        float st[kDnCols] = {buf[r % kDnPf][0].x, buf[r % kDnPf][0].y, buf[r % kDnPf][0].z, buf[r % kDnPf][0].w,
+                             buf[r % kDnPf][1].x, buf[r % kDnPf][1].y, buf[r % kDnPf][1].z, buf[r % kDnPf][1].w};
+        if (r + kDnPf < kDnRows) {
+            const float* src = S + (size_t)(rbase + 4 * (r + kDnPf)) * kSsmDk;
+            buf[r % kDnPf][0] = *reinterpret_cast<const float4*>(src);
+            buf[r % kDnPf][1] = *reinterpret_cast<const float4*>(src + kSsmDk / 2);
+        }
+        o_lds[vl][rbase + 4 * r] = dn_row(st, k, q, decay, beta, conv_lds[256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
+        float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
+        *reinterpret_cast<float4*>(dst) = make_float4(st[0], st[1], st[2], st[3]);
+        *reinterpret_cast<float4*>(dst + kSsmDk / 2) = make_float4(st[4], st[5], st[6], st[7]);
+    }
+    __syncthreads();
+    dn_norm_out(a, o_lds[vl], lane, wi, vh, (size_t)s * (kSsmVHeads * kSsmDv), z);
+}
+
+// ---------------------------------------------------------------------------
 // Gather: work item = (sequence, 32 consecutive output tokens), split over 8
 // workgroups = (K or V) x (8-token quarter); output rows are [tok][kv_head][d]
 // packed back to back.  A workgroup moves 16 KiB: each thread 4 x 16 B, all
@@ -1455,6 +1747,23 @@ int launch_qkv_append(const QkvArgs& a, void* stream) {
         hipLaunchKernelGGL(qkv_append_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
     else
         hipLaunchKernelGGL(qkv_append_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+
+int launch_deltanet(const DeltaNetArgs& a, void* stream) {
+    static_assert(kSsmVHeads == 2 * kSsmKHeads && kSsmDk == 128 && kSsmDv == 128,
+                  "one workgroup per k-head and its two v-heads, 4 columns per lane");
+    const dim3 grid(a.n_seqs * kSsmKHeads), block(kDnThreads);
+    if (a.n_tok == 1) {
+        if (a.in_bf16)
+            hipLaunchKernelGGL(deltanet_decode_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(deltanet_decode_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
+    } else if (a.in_bf16) {
+        hipLaunchKernelGGL(deltanet_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
+    } else {
+        hipLaunchKernelGGL(deltanet_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
+    }
     return (int)hipGetLastError();
 }
 

@@ -42,7 +42,7 @@ EXPORTS = [
     "kvc_get_stats", "kvc_abi_version", "kvc_seq_create", "kvc_seq_release",
     "kvc_seq_reset", "kvc_seq_len", "kvc_seq_truncate", "kvc_seq_reserve",
     "kvc_seq_commit", "kvc_prefix_match", "kvc_append", "kvc_qkv_append", "kvc_decode_attn",
-    "kvc_prefill_attn", "kvc_gather", "kvc_state_ptrs", "kvc_snapshot_save",
+    "kvc_prefill_attn", "kvc_gather", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
     "kvc_snapshot_restore", "kvc_snapshot_release", "kvc_pool_fill_normal",
     "kvc_fill_normal_bf16", "kvc_sync",
 ]
@@ -115,6 +115,7 @@ def lib() -> ctypes.CDLL:
             "kvc_prefill_attn": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P, I32, F32, P]),
             "kvc_gather": (ctypes.c_int, [P, I32, pI32, I32, I32, pI32, P, P, P]),
             "kvc_state_ptrs": (ctypes.c_int, [P, I32, I32, ctypes.POINTER(P), ctypes.POINTER(P)]),
+            "kvc_deltanet_step": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, P, P, I32, P]),
             "kvc_snapshot_save": (ctypes.c_int, [P, pI32, I32, pI32, P]),
             "kvc_snapshot_restore": (ctypes.c_int, [P, pI32, pI32, I32, P]),
             "kvc_snapshot_release": (ctypes.c_int, [P, I32]),
@@ -389,6 +390,12 @@ class Context:
         r, c = ctypes.c_void_p(), ctypes.c_void_p()
         _check(self.L.kvc_state_ptrs(self.ptr, s, ssm_layer, ctypes.byref(r), ctypes.byref(c)))
         return r.value, c.value
+
+    def deltanet_step(self, ssm_layer, seqs, n_tok, proj, conv_w, dt_bias, a, norm_w, out,
+                      in_dtype=DTYPE_BF16, out_dtype=DTYPE_F32, stream=None):
+        _check(self.L.kvc_deltanet_step(self.ptr, ssm_layer, _i32(seqs), len(seqs), n_tok, self._p(proj),
+                                        in_dtype, self._p(conv_w), self._p(dt_bias), self._p(a),
+                                        self._p(norm_w), self._p(out), out_dtype, stream))
 
     def snapshot_save(self, seqs, stream=None):
         ids = (ctypes.c_int32 * len(seqs))()

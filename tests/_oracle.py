@@ -64,6 +64,7 @@ def L() -> ctypes.CDLL:
             "orc_rms_norm_head": (None, [P, I, P, F]),
             "orc_rope_head": (None, [P, I, P, P]),
             "orc_qkv_produce": (None, [P, I, I, I, I, P, P, F, P, P, P, P, P, P]),
+            "orc_deltanet_layer_step": (None, [P, P, P, P, P, P, P, I, I, I, I, F, F, I, P]),
         }
         for n, (r, a) in sigs.items():
             f = getattr(lib, n)
@@ -174,6 +175,27 @@ def qkv_produce(qkv_row, q_norm, k_norm, cos_row, sin_row, n_q=16, n_kv=4, d=256
     L().orc_qkv_produce(_p(row), n_q, n_kv, d, rope_dim, _p(qn), _p(kn), eps, _p(c), _p(s_),
                         _p(q), _p(g), _p(k), _p(v))
     return q, g, k, v
+
+
+# ---- Gated-DeltaNet layer (src/engine.cpp:3197-3327) -------------------------
+
+SSM_NV, SSM_NK, SSM_DK, SSM_DV = 32, 16, 128, 128  # src/model_config.h:25-31
+SSM_C = 2 * SSM_NK * SSM_DK + SSM_NV * SSM_DV      # 8192 conv channels
+SSM_PROJ = SSM_C + SSM_NV * SSM_DV + 2 * SSM_NV    # 12352 projection rows per token
+SSM_SCALE = 1.0 / 11.3137                         # :3251
+
+
+def deltanet_layer_step(conv_state, ssm_state, proj, conv_w, dt_bias, a, norm_w, n_v=SSM_NV, n_k=SSM_NK,
+                        dk=SSM_DK, dv=SSM_DV, eps=RMS_EPS, fast=0):
+    """One token through one layer; conv_state / ssm_state (fp32) are updated
+    in place; returns the gated-RMSNorm output [n_v * dv]."""
+    for arr in (conv_state, ssm_state):
+        assert arr.dtype == np.float32 and arr.flags.c_contiguous
+    f = [np.ascontiguousarray(x_, dtype=np.float32) for x_ in (proj, conv_w, dt_bias, a, norm_w)]
+    out = np.empty(n_v * dv, np.float32)
+    L().orc_deltanet_layer_step(_p(conv_state), _p(ssm_state), _p(f[0]), _p(f[1]), _p(f[2]), _p(f[3]),
+                                _p(f[4]), n_v, n_k, dk, dv, eps, np.float32(SSM_SCALE), fast, _p(out))
+    return out
 
 
 def reference_prefix(cached, prompt):
