@@ -10,18 +10,21 @@
 //   load_model_and_tokenizer   cache + state allocation   src/engine.cpp:3835-3843
 //   generate                   prompt truncation           :4048-4056
 //                              prefix reuse                :4058-4080
-//                              batched prefill (32/batch)  :2843-2929 (append :2885, attention :2892)
-//                              decode loop                 :3521-3564, :4133-4151
+//                              batched prefill (32/batch)  :2843-2929
+//                              decode loop                 :3478-3564, :4133-4151
 //   reset_state                                            :4164-4176
 //
-// Everything outside the KV path is synthetic, because no model weights are
-// available: a token's q, gate, K and V in every attention layer are N(0,1)
-// values drawn from (seed, layer, token id, position), and the next token is
-// drawn from the token history and a digest of the recurrent state.  A
-// Gated-DeltaNet layer's state is represented by that digest, written into
-// the first two words of its recurrent state on the device at every step, so
-// snapshot/restore of the real state buffers decides what a resumed request
-// generates.  The attention outputs of every step are kept for inspection.
+// Per attention layer and token the engine calls what the reference does at
+// those sites: the producer + append (kvc_qkv_append: q/k RMSNorm, RoPE, K/V
+// append; :3485-3525, :2846-2889), then prefill or decode attention.  Per
+// Gated-DeltaNet layer it runs the layer step on the live recurrent state
+// (kvc_deltanet_step; :3197-3327, :2600-2716).  Everything outside the KV path
+// is synthetic, because no model weights are available: a token's projection
+// rows (the attention qkv row and the DeltaNet row) are N(0,1) values drawn
+// from (seed, layer, token id, position), the norm / conv / gate weights are
+// seeded too, and the next token is drawn from the token history and the last
+// token's layer outputs.  A resumed request therefore generates what a fresh
+// one does only if the cached K/V and the restored recurrent state are exact.
 #pragma once
 
 #include <cstdint>
@@ -46,6 +49,8 @@ struct EngineConfig {
     double pool_fraction = 0.05; // share of free HBM for the K/V pools
     uint64_t seed = 1;           // synthetic projections and sampling
     bool keep_outputs = true;    // keep every step's attention outputs
+    bool verify_restore = false; // hash the recurrent state at snapshot boundaries and
+                                 // check restored states against it (costly)
     bool verbose = false;        // print the reference's progress lines
 };
 
@@ -66,22 +71,31 @@ double get_last_prefill_ms();
 int pos();                                  // g_pos
 const std::vector<int>& cached_tokens();    // g_cached_tokens
 int last_prefix_len();                      // tokens reused by the last generate()
-int state_restore_mismatches();             // resumed states that differ from recomputation
+int state_restore_mismatches();             // restored states that differ from the state hashed
+                                            // when their boundary was processed (verify_restore)
+int state_restore_checks();                 // restored states compared
 kvc_ctx* context();
 int32_t sequence();
 
 // One processed position: the attention output (bf16 bits, [16 q heads][256])
-// of every attention layer, and which kernel produced it.
+// of every attention layer, the Gated-DeltaNet output ([4096]) of every
+// recurrent layer, and which kernels produced them.  Decode steps also keep
+// the producer's q and gate rows of every attention layer.
 struct StepOutput {
     int pos = 0;
     bool from_prefill = false;
-    std::vector<std::vector<uint16_t>> out;  // [layer][16 * 256]
+    std::vector<std::vector<uint16_t>> out;      // [attn layer][16 * 256]
+    std::vector<std::vector<uint16_t>> ssm_out;  // [ssm layer][32 * 128]
+    std::vector<std::vector<uint16_t>> q, gate;  // [attn layer][16 * 256], decode steps only
 };
 const std::vector<StepOutput>& step_outputs();  // positions processed by the last generate()
 
-// The synthetic projections of one token (bf16 bits), as the engine appends
-// and queries them: q, gate [16][256]; k, v [4][256].
-void synthetic_projection(int layer, int token, int pos, std::vector<uint16_t>& q, std::vector<uint16_t>& gate,
-                          std::vector<uint16_t>& k, std::vector<uint16_t>& v);
+// Width of the synthetic attention projection row: [16][q | gate][256], k [4][256], v [4][256].
+constexpr int kQkvRow = 16 * 2 * 256 + 2 * 4 * 256;
+// The synthetic attention projection row of one token (bf16 bits) and the
+// layer's q_norm / k_norm weights (fp32 [256] each), as the engine hands them
+// to kvc_qkv_append.
+void synthetic_qkv_row(int layer, int token, int pos, std::vector<uint16_t>& row);
+void synthetic_norm_weights(int layer, std::vector<float>& q_norm, std::vector<float>& k_norm);
 
 }  // namespace kvengine
