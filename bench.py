@@ -282,6 +282,89 @@ def cpu_baseline_decode(Ls, budget_s):
     return dt / n, cores
 
 
+def _oracle():
+    sys.path.insert(0, str(ROOT / "tests"))
+    import _oracle as O
+    return O
+
+
+def cpu_baseline_c(P, n_q=128):
+    """Config c on the oracle, bounded samples: the gather as memcpy of the
+    reused K/V (1 thread, 8 sessions), the causal prefill of one session per
+    core (threads), and the producer (q/k RMSNorm + RoPE) of 256 tokens."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    O = _oracle()
+    cores = host_cores()
+    # gather: reference-layout copies of 8 sessions' reused K and V
+    srcs = [np.ones(int(p_) * ROW, np.uint16) for p_ in P[:8]]
+    dsts = [np.zeros_like(x_) for x_ in srcs]  # touched before the clock starts
+    t0 = time.perf_counter()
+    for src, dst in zip(srcs, dsts):
+        for _ in range(2):  # K and V
+            np.copyto(dst, src)
+    g_s = time.perf_counter() - t0
+    g_bytes = 2 * 2 * sum(int(p_) for p_ in P[:8]) * ROW * 2
+    # prefill: one session per core, 128 queries over P + 128 keys
+    samp = [int(x) for x in P[:cores]]
+    data = [(O.normal_bf16(n_q * NQ * D, SEED + 400 + i), O.normal_bf16((p_ + n_q) * ROW, SEED + 500 + i),
+             O.normal_bf16((p_ + n_q) * ROW, SEED + 600 + i)) for i, p_ in enumerate(samp)]
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(cores) as ex:
+        list(ex.map(lambda a: O.prefill_attn(a[1][0], a[1][1], a[1][2], samp[a[0]], n_q), enumerate(data)))
+    p_s = time.perf_counter() - t0
+    p_flops = float(sum(16384 * (128 * p_ + 8256) for p_ in samp))
+    all_flops = float(sum(16384 * (128 * int(p_) + 8256) for p_ in P))
+    # producer: 256 tokens, 1 thread
+    row = O.bf16_to_f32(O.normal_bf16(NQ * 2 * D + 2 * ROW, SEED + 700))
+    w = np.ones(D, np.float32)
+    c_t, s_t = O.rope_tables(2048)
+    t0 = time.perf_counter()
+    for t in range(256):
+        O.qkv_produce(row, w, w, c_t[t], s_t[t])
+    q_s = time.perf_counter() - t0
+    q_bytes = 256 * ((NQ * 2 * D + 2 * ROW) * 2 + 2 * NQ * D * 2 + 2 * ROW * 2)
+    return {"kind": "port", "cores": cores,
+            "gather_GBps": round(g_bytes / g_s / 1e9, 2),
+            "prefill_TFLOPs": round(p_flops / p_s / 1e12, 4),
+            "prefill_us_per_layer": round(all_flops / (p_flops / p_s) * 1e6, 1),
+            "qkv_append_GBps_1thread": round(q_bytes / q_s / 1e9, 3),
+            "sample": f"gather of 8 sessions (1 thread); oracle causal prefill of {len(samp)} sessions, one per "
+                      f"thread, scaled to the 64 sessions' flops; producer of 256 tokens (1 thread) "
+                      f"({cpu_model()})"}
+
+
+def cpu_baseline_e(n_sessions=64):
+    """Config e on the host: the snapshot copy (61 MB per session, 1 thread,
+    4 sessions) and the Gated-DeltaNet resume step on the oracle (one layer of
+    one session per core, threads, scaled to 64 sessions)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    O = _oracle()
+    cores = host_cores()
+    per_sess = 61079552
+    src = np.ones(per_sess // 4, np.float32)
+    dst = np.zeros_like(src)  # touched before the clock starts
+    t0 = time.perf_counter()
+    for _ in range(4):
+        np.copyto(dst, src)
+    c_s = time.perf_counter() - t0
+    rng = np.random.default_rng(SEED + 800)
+    w = [(0.5 * rng.standard_normal((4, O.SSM_C))).astype(np.float32), rng.standard_normal(O.SSM_NV).astype(np.float32),
+         -rng.uniform(0.05, 1.0, O.SSM_NV).astype(np.float32), np.ones(O.SSM_DV, np.float32)]
+    jobs = [(np.zeros((3, O.SSM_C), np.float32), np.zeros((O.SSM_NV, O.SSM_DV, O.SSM_DK), np.float32),
+             rng.standard_normal(O.SSM_PROJ).astype(np.float32)) for _ in range(cores)]
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(cores) as ex:
+        list(ex.map(lambda j: O.deltanet_layer_step(j[0], j[1], j[2], *w), jobs))
+    d_s = time.perf_counter() - t0
+    return {"kind": "port", "cores": cores,
+            "snapshot_GBps_1thread": round(2 * 4 * per_sess / c_s / 1e9, 2),
+            "resume_decode_us_per_layer": round(d_s * n_sessions / cores * 1e6, 1),
+            "sample": f"4 session snapshots copied (1 thread); the oracle's Gated-DeltaNet step of one layer for "
+                      f"{cores} sessions, one per thread, scaled to {n_sessions} ({cpu_model()})"}
+
+
 def run_d(args):
     import kvc
 
@@ -462,7 +545,8 @@ def run_c(args):
             "prefill_us_per_layer": round(p_us, 1),
             "prefill_TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 2),
             "prefill_GBps": round(p_bytes / (p_us * 1e-6) / 1e9, 1),
-            "mean_prefix": float(P.mean())}
+            "mean_prefix": float(P.mean()),
+            **({} if args.no_cpu else {"cpu_baseline": cpu_baseline_c(P)})}
 
 
 # ---------------------------------------------------------------------------
@@ -567,7 +651,8 @@ def run_e(args):
             "resume_chunk128_us_per_layer": round(dn_us["chunk"], 1),
             "resume_chunk128_GBps": round(chunk_bytes / (dn_us["chunk"] * 1e-6) / 1e9, 1),
             "resume_chunk128_TFLOPs": round(chunk_flops / (dn_us["chunk"] * 1e-6) / 1e12, 2),
-            "hbm_context_bytes": int(st.hbm_bytes)}
+            "hbm_context_bytes": int(st.hbm_bytes),
+            **({} if args.no_cpu else {"cpu_baseline": cpu_baseline_e()})}
 
 
 # ---------------------------------------------------------------------------
