@@ -1183,7 +1183,10 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
     // every input row of this lane is requested before anything is stored:
     // rows 4w + 2i + sub of [q 0..15, k 0..3] (normalized) and of
     // [gate 0..15, v 0..3] (copied)
+    // copied rows of bf16 input go through as raw 16-B pieces (RNE of a bf16
+    // value is itself); fp32 input is converted
     float x[2][8], c[2][8];
+    u32x4 craw[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int r = wave * 4 + i * 2 + sub;
@@ -1191,7 +1194,13 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
         const size_t co = kv_wave ? row + kKOff + (size_t)(kKvHeads + r - kQHeads) * kHeadDim
                                   : row + (size_t)r * 2 * kHeadDim + kHeadDim;
         load_row8<BF16IN>(a.qkv, xo + d0, x[i]);
-        if (kv_wave || a.gate_out) load_row8<BF16IN>(a.qkv, co + d0, c[i]);
+        if (kv_wave || a.gate_out) {
+            if constexpr (BF16IN)
+                craw[i] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qkv) + co + d0));
+            else
+                load_row8<BF16IN>(a.qkv, co + d0, c[i]);
+        }
     }
     const int blk = a.table[(size_t)a.slot[s] * a.table_stride + pos / kBlockTok];
     // RoPE coefficients of this lane's 8 dims: table entries p0 .. p0+7 for
@@ -1230,9 +1239,15 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
         if (kv_wave) {
             const size_t slot =
                 (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
-            store_bf16x8(a.vpool + slot, c[i]);
+            if constexpr (BF16IN)
+                __builtin_nontemporal_store(craw[i], reinterpret_cast<u32x4*>(a.vpool + slot));
+            else
+                store_bf16x8(a.vpool + slot, c[i]);
         } else if (a.gate_out) {
-            store_bf16x8(a.gate_out + orow + (size_t)r * kHeadDim + d0, c[i]);
+            if constexpr (BF16IN)
+                __builtin_nontemporal_store(craw[i], reinterpret_cast<u32x4*>(a.gate_out + orow + (size_t)r * kHeadDim + d0));
+            else
+                store_bf16x8(a.gate_out + orow + (size_t)r * kHeadDim + d0, c[i]);
         }
     }
     // normalized rows: RMSNorm, RoPE, bf16
