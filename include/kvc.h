@@ -135,7 +135,12 @@ int kvc_abi_version(void);
 /* ---- sequences ------------------------------------------------------------ */
 int kvc_seq_create(kvc_ctx* ctx, int32_t* seq);
 int kvc_seq_release(kvc_ctx* ctx, int32_t seq);
-/* reset_state(): length 0, blocks released, no memset (src/engine.cpp:4164) */
+/* reset_state(): length 0, blocks released (src/engine.cpp:4164).  No memset
+ * here: the recurrent/conv state of a created or reset sequence reads as zero
+ * from its next use on (the Gated-DeltaNet step, a snapshot save or
+ * kvc_state_ptrs zero-fill it first, on their stream), unless a snapshot
+ * restore writes it.  A graph captured around such a first use would replay
+ * the fill: capture after it. */
 int kvc_seq_reset(kvc_ctx* ctx, int32_t seq);
 int kvc_seq_len(kvc_ctx* ctx, int32_t seq, int32_t* len);
 /* Drop tokens beyond len (rollback); len <= current length. */

@@ -83,6 +83,7 @@ struct Seq {
     std::vector<int32_t> blocks;   // block id per 32-token block
     std::vector<int32_t> tokens;   // committed token ids (when known)
     std::vector<int32_t> entries;  // prefix-index entry per full block, -1 = none
+    bool state_dirty = false;      // recurrent state must be zeroed before its next use
 };
 
 struct Entry {
@@ -322,10 +323,44 @@ void release_tail(kvc_ctx* c, int32_t slot, int32_t keep_blocks) {
     }
 }
 
+// A created or reset sequence's recurrent state reads as zero (reset_state()
+// zero-fills it, src/engine.cpp:4164-4176).  The fill is deferred to the first
+// operation that uses the state, on that operation's stream: the Gated-DeltaNet
+// step, a snapshot save, kvc_state_ptrs.  A snapshot restore overwrites the
+// whole state and clears the flag.
+int clean_states(kvc_ctx* c, const int32_t* seqs, size_t n, void* stream) {
+    if (!c->has_device || c->state_bytes == 0) return KVC_OK;
+    ZeroStateArgs z{};
+    z.state = c->d_state;
+    z.state_bytes = c->state_bytes;
+    for (size_t i = 0; i < n; i++) {
+        Seq& s = c->seqs[seqs[i]];
+        if (!s.state_dirty) continue;
+        s.state_dirty = false;
+        z.slot[z.n_slots++] = seqs[i];
+        if (z.n_slots == kMaxBatch || i + 1 == n) {
+            int e = launch_zero_state(z, stream);
+            if (e) return hip_err((hipError_t)e, "state zero-fill launch");
+            z.n_slots = 0;
+        }
+    }
+    if (z.n_slots > 0) {
+        int e = launch_zero_state(z, stream);
+        if (e) return hip_err((hipError_t)e, "state zero-fill launch");
+    }
+    return KVC_OK;
+}
+
 int launch_snapshots(kvc_ctx* c, const std::vector<int32_t>& seq_slots,
                      const std::vector<int32_t>& snap_slots, const std::vector<int32_t>& first_blocks,
                      bool restore, bool do_state, bool do_kv, void* stream) {
     if (!c->has_device) return KVC_OK;
+    if (do_state && !restore) {  // a save reads the state: it must hold its zeros
+        int rc = clean_states(c, seq_slots.data(), seq_slots.size(), stream);
+        if (rc) return rc;
+    }
+    if (do_state && restore)
+        for (int32_t s : seq_slots) c->seqs[s].state_dirty = false;  // overwritten below
     for (size_t i0 = 0; i0 < seq_slots.size(); i0 += kMaxBatch) {
         SnapshotArgs a{};
         a.state_base = c->d_state;
@@ -669,6 +704,7 @@ int kvc_seq_create(kvc_ctx* c, int32_t* seq) {
     c->free_seqs.pop_back();
     c->seqs[s] = Seq();
     c->seqs[s].live = true;
+    c->seqs[s].state_dirty = c->cfg.n_ssm_layers > 0;  // the slot may hold an earlier sequence's state
     *seq = s;
     return KVC_OK;
 }
@@ -681,6 +717,7 @@ int kvc_seq_reset(kvc_ctx* c, int32_t seq) {
     s.tokens.clear();
     s.entries.clear();
     s.tokens_known = true;
+    s.state_dirty = c->cfg.n_ssm_layers > 0;
     return KVC_OK;
 }
 
@@ -1178,6 +1215,11 @@ int kvc_state_ptrs(kvc_ctx* c, int32_t seq, int32_t ssm_layer, void** rec, void*
     if (!seq_ok(c, seq)) return set_err(KVC_ERR_INVALID, "sequence %d is not live", seq);
     if (ssm_layer < 0 || ssm_layer >= c->cfg.n_ssm_layers)
         return set_err(KVC_ERR_RANGE, "ssm layer %d out of range [0, %d)", ssm_layer, c->cfg.n_ssm_layers);
+    if (c->seqs[seq].state_dirty) {  // hand out zeros, finished
+        if ((rc = clean_states(c, &seq, 1, nullptr))) return rc;
+        hipError_t e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) return hip_err(e, "state zero-fill");
+    }
     uint8_t* base = c->d_state + (int64_t)seq * c->state_bytes + (int64_t)ssm_layer * (c->rec_bytes + c->conv_bytes);
     if (rec) *rec = base;
     if (conv) *conv = base + c->rec_bytes;
@@ -1204,6 +1246,7 @@ int kvc_deltanet_step(kvc_ctx* c, int32_t ssm_layer, const int32_t* seqs, int32_
         (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16))
         return set_err(KVC_ERR_INVALID, "bad in_dtype / out_dtype");
     const size_t isz = in_dtype == KVC_DTYPE_BF16 ? 2 : 4, osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
+    if ((rc = clean_states(c, seqs, (size_t)n_seqs, stream))) return rc;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
         const int32_t n = std::min(kMaxBatch, n_seqs - i0);
         DeltaNetArgs d{};

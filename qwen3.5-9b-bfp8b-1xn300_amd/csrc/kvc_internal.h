@@ -145,6 +145,14 @@ struct DeltaNetArgs {
     int32_t slot[kMaxBatch];
 };
 
+struct ZeroStateArgs {
+    uint8_t* state;       // state pool base
+    int64_t state_bytes;  // per sequence slot (multiple of 256)
+    int32_t n_slots;
+    int32_t pad;
+    int32_t slot[kMaxBatch];
+};
+
 struct GatherArgs {
     const uint16_t* kpool;
     const uint16_t* vpool;
@@ -220,6 +228,7 @@ int launch_decode(const DecodeArgs& a, void* stream);
 int launch_append(const AppendArgs& a, void* stream);
 int launch_qkv_append(const QkvArgs& a, void* stream);
 int launch_deltanet(const DeltaNetArgs& a, void* stream);
+int launch_zero_state(const ZeroStateArgs& a, void* stream);
 int launch_gather(const GatherArgs& a, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_snapshot(const SnapshotArgs& a, void* stream);

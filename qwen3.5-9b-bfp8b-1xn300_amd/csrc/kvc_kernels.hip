@@ -1589,6 +1589,17 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArg
 }
 
 // ---------------------------------------------------------------------------
+// Zero-fill of whole per-sequence state slots: a fresh or reset sequence's
+// recurrent and conv state starts at zero, as reset_state() zero-fills it
+// (src/engine.cpp:4164-4176).  Grid (pieces, slot), 16 B per thread per step.
+__global__ __launch_bounds__(256) void zero_state_kernel(ZeroStateArgs a) {
+    uint4* base = reinterpret_cast<uint4*>(a.state + (size_t)a.slot[blockIdx.y] * a.state_bytes);
+    const size_t n = (size_t)a.state_bytes / 16;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        base[i] = make_uint4(0, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
 // Gather: work item = (sequence, 32 consecutive output tokens), split over 8
 // workgroups = (K or V) x (8-token quarter); output rows are [tok][kv_head][d]
 // packed back to back.  A workgroup moves 16 KiB: each thread 4 x 16 B, all
@@ -1779,6 +1790,11 @@ int launch_deltanet(const DeltaNetArgs& a, void* stream) {
     } else {
         hipLaunchKernelGGL(deltanet_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
     }
+    return (int)hipGetLastError();
+}
+
+int launch_zero_state(const ZeroStateArgs& a, void* stream) {
+    hipLaunchKernelGGL(zero_state_kernel, dim3(512, a.n_slots), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 

@@ -332,18 +332,13 @@ bool load_model_and_tokenizer(const EngineConfig& cfg) {
 
 // src/engine.cpp:4164-4176: the reference zero-fills every cache and state
 // array; here the sequence drops its block references (its blocks stay in the
-// prefix index for later requests) and its recurrent state is zeroed.
+// prefix index for later requests), and libkvc zero-fills its recurrent state
+// before the next Gated-DeltaNet step unless a snapshot restore replaces it.
 void reset_state() {
     if (!g_loaded) return;
     kvc_ok(kvc_seq_reset(g_ctx, g_seq), "kvc_seq_reset");
     g_cached_tokens.clear();
     g_out_digest = 0;
-    for (int l = 0; l < g_cfg.n_ssm_layers; l++) {
-        void *rec = nullptr, *conv = nullptr;
-        if (!kvc_ok(kvc_state_ptrs(g_ctx, g_seq, l, &rec, &conv), "kvc_state_ptrs")) return;
-        hip_ok(hipMemset(rec, 0, (size_t)kSsmVHeads * kSsmDv * kSsmDk * 4), "state reset");
-        hip_ok(hipMemset(conv, 0, (size_t)3 * kSsmC * 4), "state reset");
-    }
 }
 
 void shutdown() {

@@ -158,3 +158,86 @@ def test_deltanet_resume_from_snapshot_is_bit_identical():
         ctx.snapshot_release(ids[0])
         for b_ in bufs + [ob]:
             b_.free()
+
+
+def test_deltanet_state_is_zero_after_create_and_reset():
+    """A created or reset sequence's recurrent and conv state reads as zero
+    (reset_state() zero-fills it, src/engine.cpp:4164-4176), whatever the slot
+    held before: the next layer step runs from zeros, kvc_state_ptrs shows
+    zeros, a snapshot saved after the reset holds zeros, and a snapshot
+    restored after the reset wins over the pending zero-fill."""
+    say("deltanet state zeroed on create/reset")
+    h = kvc.hip()
+    rng = np.random.default_rng(7500)
+    conv_w, dtb, a, nw = weights(7501)
+    proj32 = rng.standard_normal((3, PROJ)).astype(np.float32)
+    bufs = [kvc.to_device(x_) for x_ in (proj32, conv_w, dtb, a, nw)]
+    ob = h.malloc(3 * NV * DV * 4)
+
+    def read(s, layer):
+        rb, cb = state_bufs(ctx, s, layer)
+        return rb.download(np.float32, (NV, DV, DK)), cb.download(np.float32, (3, C))
+
+    def is_zero(s):
+        return all(not x_.any() for layer in range(2) for x_ in read(s, layer))
+
+    with ctx_ssm(max_seqs=1) as ctx:  # one slot: every create reuses it
+        s = ctx.seq_create()
+        fill_seq(ctx, Mirror(1), [s], 256, seed=7502)
+        saved = []
+        for layer in range(2):
+            rb, cb = state_bufs(ctx, s, layer)
+            S = (0.05 * rng.standard_normal((NV, DV, DK))).astype(np.float32)
+            cw = rng.standard_normal((3, C)).astype(np.float32)
+            rb.upload(S)
+            cb.upload(cw)
+            saved.append((S, cw))
+        ida = ctx.snapshot_save([s])[0]
+        ctx.deltanet_step(1, [s], 2, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], ob, in_dtype=kvc.DTYPE_F32)
+        ctx.sync()
+
+        # reset, then step: the step starts from zero state
+        ctx.seq_reset(s)
+        ctx.deltanet_step(1, [s], 3, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], ob, in_dtype=kvc.DTYPE_F32)
+        ctx.sync()
+        out = ob.download(np.float32, (3, NV * DV))
+        cs, S = np.zeros((3, C), np.float32), np.zeros((NV, DV, DK), np.float32)
+        for t in range(3):
+            rel_close(out[t], O.deltanet_layer_step(cs, S, proj32[t], conv_w, dtb, a, nw), f"after reset, tok {t}")
+        r1, c1 = read(s, 1)
+        assert np.array_equal(c1, cs)
+        rel_close(r1, S, "state after reset + 3 tokens")
+        r0, c0 = read(s, 0)  # the other layer was zeroed with it
+        assert not r0.any() and not c0.any()
+
+        # reset, then restore: the snapshot's state, not zeros
+        ctx.seq_reset(s)
+        ctx.snapshot_restore([s], [ida])
+        ctx.sync()
+        for layer in range(2):
+            r, c = read(s, layer)
+            assert np.array_equal(r, saved[layer][0]) and np.array_equal(c, saved[layer][1]), f"layer {layer}"
+        ctx.snapshot_release(ida)
+
+        # release + create on the same slot: zeros; a snapshot saved now holds zeros
+        ctx.seq_release(s)
+        s2 = ctx.seq_create()
+        assert s2 == s
+        fill_seq(ctx, Mirror(1), [s2], 256, seed=7503)
+        idb = ctx.snapshot_save([s2])[0]
+        for layer in range(2):
+            rb, cb = state_bufs(ctx, s2, layer)
+            rb.upload(saved[layer][0])
+            cb.upload(saved[layer][1])
+        ctx.snapshot_restore([s2], [idb])
+        ctx.sync()
+        assert is_zero(s2)
+        ctx.snapshot_release(idb)
+        for layer in range(2):
+            rb, cb = state_bufs(ctx, s2, layer)
+            rb.upload(saved[layer][0])
+            cb.upload(saved[layer][1])
+        ctx.seq_reset(s2)
+        assert is_zero(s2)  # kvc_state_ptrs finishes the fill before returning
+    for b_ in bufs + [ob]:
+        b_.free()
