@@ -758,8 +758,9 @@ constexpr int kSgDsRead = 0x100;            //   LDS read
 #endif
 constexpr int kPfNT = KVC_PF_NT;            // 16-row query tiles per prefill wave (1 or 2)
 
-struct PrefillSmem {
-    uint16_t kv[2][2][kTileElems];  // [buffer][K | V][row * 256 + swizzled column]
+struct PrefillSmem {  // [buffer][row * 256 + swizzled column]; V first, so V^T reads reach
+    uint16_t v[2][kTileElems];   // both buffers with 16-bit immediate offsets from one base
+    uint16_t k[2][kTileElems];
 };
 
 // Tile swizzles: 16-B chunk c of row r sits at position c ^ kswz(r) (K) or
@@ -774,14 +775,16 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4 v) { return __builtin_bit_ca
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// 16 B per lane from global memory straight into LDS (global_load_lds_dwordx4;
-// lane i writes LDS bytes [lds_off + 16i, +16)).  Issued from inline asm so
-// the compiler does not treat the in-flight copy as a pending write to every
-// LDS object (it would otherwise wait for it before the current tile's
-// reads); callers order it with an explicit s_waitcnt vmcnt(0) and barrier.
-// M0 is set here and used by nothing else in the prefill kernel.
-__device__ __forceinline__ void lds_dma16(const void* gptr, uint32_t lds_off) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_off), "v"(gptr)
+// 16 B per lane from global memory straight into LDS (global_load_lds_dwordx4,
+// scalar-base form): lane i copies gbase + voff[i] (gbase uniform, in SGPRs)
+// into LDS bytes [lds_off + 16i, +16).  Issued from inline asm so the
+// compiler does not treat the in-flight copy as a pending write to every LDS
+// object (it would otherwise wait for it before the current tile's reads);
+// callers order it with an explicit s_waitcnt vmcnt(0) and barrier.  M0 is
+// set here and used by nothing else in the prefill kernel.
+__device__ __forceinline__ void lds_dma16s(const void* gbase, uint32_t voff, uint32_t lds_off) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_off), "v"(voff),
+                 "s"(gbase)
                  : "memory");
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -802,6 +805,25 @@ __device__ __forceinline__ u32x2 lds_load_tr16(uint32_t base, uint32_t off) {
 // NT = 16-row query tiles per wave: NT = 2 runs 4 waves (one per q head of
 // the group, 32 rows each); NT = 1 runs 8 waves (q head, row half), two per
 // SIMD, so one wave's MFMAs overlap the other's LDS reads and softmax.
+//
+// The per-tile VALU work is kept small:
+//  - full tiles are fetched with the scalar-base form of the LDS DMA, with
+//    per-lane offsets fixed at kernel start (only a tile that runs past the
+//    last key clamps rows per lane);
+//  - the loop is unrolled over the two buffers, so every operand-fragment
+//    address is a per-lane base plus an immediate;
+//  - scores stay unscaled on full tiles: the tile max is scaled once and the
+//    scale enters the exponent through an FMA (a negative scale is moved into
+//    Q, whose sign flip is exact, so the scale used is |scale| >= 0); only
+//    tiles that reach the diagonal or the sequence end are masked;
+//  - the softmax denominator comes from two more MFMAs per tile, with an
+//    all-ones A operand against the same bf16 P^T (so it sums exactly the
+//    weights that P.V uses).
+template <int B>
+struct PfBuf {
+    static constexpr int value = B;
+};
+
 template <int NT>
 __global__ __launch_bounds__(64 * 8 / NT) __attribute__((amdgpu_waves_per_eu(2 / NT, 2 / NT)))
 void prefill_mfma_kernel(PrefillArgs a) {
@@ -834,6 +856,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
     const int n_blocks = (kmax + kBlockTok - 1) / kBlockTok;
     const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
     constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
+    const float c = fabsf(a.scale_log2);
+    const uint32_t qflip = a.scale_log2 < 0.f ? 0x80008000u : 0u;
 
     // Q^T as the B operand: qb[nt][ks] = q[row rw0 + 16nt + r16][d 32ks + 8q4 .. +7]
     bf16x8_t qb[NT][8];
@@ -842,8 +866,14 @@ void prefill_mfma_kernel(PrefillArgs a) {
         const int r = row0 + min(rw0 + 16 * nt + r16, rows - 1);
         const uint16_t* qr = a.q + (((size_t)s * a.n_q + r) * kQHeads + h * kGroup + g) * kHeadDim;
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++)
-            qb[nt][ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * q4));
+        for (int ks = 0; ks < 8; ks++) {
+            u32x4 x = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * q4);
+            x[0] ^= qflip;
+            x[1] ^= qflip;
+            x[2] ^= qflip;
+            x[3] ^= qflip;
+            qb[nt][ks] = as_bf16x8(x);
+        }
     }
 
     // block ids of a 64-block window sit in one VGPR (lane i = block w0 + i)
@@ -852,77 +882,79 @@ void prefill_mfma_kernel(PrefillArgs a) {
     int idv = lane < n_blocks ? trow[lane] : 0;
     // wave w loads tile rows kLoadRows*w .., two per instruction (lanes 0-31:
     // row r0, lanes 32-63: the next row); lane l fills chunk position l % 32
-    // of its row, i.e. global chunk (l % 32) ^ (row % 16)
-    auto issue_tile = [&](int t, int buf) {
-        const int last = kmax - 1 - t * kPfKeys;  // last valid row of the tile
-        const int ida = __builtin_amdgcn_readlane(idv, 2 * t - idw0);
-        const int idb = __builtin_amdgcn_readlane(idv, min(2 * t + 1, n_blocks - 1) - idw0);
+    // of its row, i.e. global chunk (l % 32) ^ swz(row).  A wave's rows lie in
+    // one of the tile's two blocks (half = 0 or 1).
+    const int half = (kLoadRows * wave) / kBlockTok;
+    // Byte offset inside a (block, head) unit of the 16 B lane l fills for
+    // instruction j: row part ((r0 & 31) + l / 32) * 512, chunk part
+    // ((l % 32) ^ swz(r)) * 16.  Since r % 16 = s0 | 2j with s0 = (r0(0) % 16)
+    // | l / 32 (disjoint bits), the chunk part is cb ^ (j * 32) for K (swz =
+    // r % 16) and cb ^ (j * 64) for V (swz = 2 (r % 16)).
+    static_assert(kLoadRows == 8 || kLoadRows == 16, "s0 and 2j occupy disjoint bits");
+    const int s0 = ((kLoadRows * wave) & 15) | (lane >> 5);
+    const uint32_t cbk = (((lane & 31) ^ s0) << 4) + (lane >> 5) * 512;
+    const uint32_t cbv = (((lane & 31) ^ (s0 << 1)) << 4) + (lane >> 5) * 512;
+    // Rows past the last key are loaded from the last key (finite data,
+    // weight 0).  The clamped rows of a wave still lie in one block: a wave
+    // of the second half reads block 2t + 1 if the last key is in it, else
+    // the last key of block 2t.
+    auto issue_rows = [&](const uint16_t* pool, uint32_t cb, int jsh, uint32_t lds_tile, int t) {
+        const int last = kmax - 1 - t * kPfKeys;  // last key row of the tile
+        const int id = __builtin_amdgcn_readlane(idv, 2 * t + (half && last >= kBlockTok ? 1 : 0) - idw0);
+        const uint16_t* base = pool + ((size_t)id * kKvHeads + h) * kUnitElems;
+        const bool full = last >= kPfKeys - 1;  // uniform
 #pragma unroll
         for (int j = 0; j < kLoadRows / 2; j++) {
             const int r0 = kLoadRows * wave + 2 * j;
-            const int r = r0 + (lane >> 5);
-            const int rs = min(r, last);
-            const size_t row = ((size_t)(rs < kBlockTok ? ida : idb) * kKvHeads + h) * kUnitElems +
-                               (rs & (kBlockTok - 1)) * kHeadDim;
-            lds_dma16(a.kpool + row + (((lane & 31) ^ kswz(r)) << 3), lds_addr(&sm.kv[buf][0][r0 * kHeadDim]));
-            lds_dma16(a.vpool + row + (((lane & 31) ^ vswz(r)) << 3), lds_addr(&sm.kv[buf][1][r0 * kHeadDim]));
+            uint32_t off = (cb ^ (j << jsh)) + (r0 & (kBlockTok - 1)) * 512;
+            if (!full) off = (min(r0 + (lane >> 5), last) & (kBlockTok - 1)) * 512 | (off & 511);
+            lds_dma16s(base, off, lds_tile + r0 * kHeadDim * 2);
         }
     };
+    auto issue_k = [&](int t, int buf) { issue_rows(a.kpool, cbk, 5, lds_addr(&sm.k[buf][0]), t); };
+    auto issue_v = [&](int t, int buf) { issue_rows(a.vpool, cbv, 6, lds_addr(&sm.v[buf][0]), t); };
 
     // With NT = 2 the accumulators outgrow the VGPRs: an (empty) statement
     // with an AGPR operand makes the compiler select the AGPR-accumulator form
     // of the MFMAs, so O^T lives in AGPRs.
     if constexpr (NT == 2) asm volatile("" ::"a"(0));
-    f32x4 o[16][NT];
-    float m_run[NT], l_lane[NT];
+    f32x4 o[16][NT], ol[NT];  // ol: the all-ones row block (softmax denominator)
+    float m_run[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
 #pragma unroll
         for (int dt = 0; dt < 16; dt++) o[dt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        ol[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
         m_run[nt] = kNegBig;
-        l_lane[nt] = 0.f;
     }
+    const bf16x8_t ones = as_bf16x8(u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
 
-    // Per-lane byte offsets of the operand fragments inside a tile (the XOR
-    // swizzles make them lane dependent, the rest are immediates):
-    //   K (kt, ks = 4hi + j): koff[j] + 256 hi + 8192 kt
-    //   V^T (dt, kk, lo/hi):  voff[dt] + 16384 kk + 8192 (hi)
-    uint32_t koff[4], voff[16];
+    // Per-lane LDS byte addresses of the operand fragments in buffer 0 (the
+    // XOR swizzles make them lane dependent); the fragment and buffer parts
+    // are immediates:
+    //   K (kt, ks = 4hi + j): kaddr[j] + 256 hi + 8192 kt + 32768 buf
+    //   V^T (dt, kk, lo/hi):  vaddr[dt] + 16384 kk + 8192 (hi) + 32768 buf
+    uint32_t kaddr[4], vaddr[16];
+    const uint32_t k0 = lds_addr(&sm.k[0][0]), v0 = lds_addr(&sm.v[0][0]);
 #pragma unroll
-    for (int j = 0; j < 4; j++) koff[j] = r16 * 512 + 16 * ((4 * j + q4) ^ r16);
+    for (int j = 0; j < 4; j++) kaddr[j] = k0 + r16 * 512 + 16 * ((4 * j + q4) ^ r16);
     {
         const int w = 4 * q4 + (r16 >> 2);  // V row % 16 of this lane
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
-            voff[dt] = w * 512 + 16 * (2 * (dt ^ w) + ((r16 & 3) >> 1)) + 8 * (r16 & 1);
+            vaddr[dt] = v0 + w * 512 + 16 * (2 * (dt ^ w) + ((r16 & 3) >> 1)) + 8 * (r16 & 1);
     }
-    const uint32_t lds_base = lds_addr(&sm.kv[0][0][0]);
 
-    issue_tile(0, 0);
-    for (int t = 0; t < n_tiles; t++) {
-        // own loads of tile t have landed; after the barrier every wave's
-        // have, and every wave is done reading buffer (t+1)&1 (tile t-1)
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (t + 1 < n_tiles) {
-            if (2 * (t + 1) + 1 - idw0 >= 64 && 2 * (t + 1) < n_blocks) {  // uniform: next id window
-                idw0 = 2 * (t + 1);
-                idv = idw0 + lane < n_blocks ? trow[idw0 + lane] : 0;
-            }
-            issue_tile(t + 1, (t + 1) & 1);
-        }
-        const uint32_t kbuf = lds_base + (t & 1) * (uint32_t)sizeof(sm.kv[0]);  // K tile of this buffer
-        const uint32_t vbuf = kbuf + (uint32_t)sizeof(sm.kv[0][0]);            // V tile
-
-        // S^T tiles: st[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16.
-        // Steps i = (ks, kt) run d-slice outer, key subtile inner, so
-        // consecutive MFMAs feed different accumulators; the 32 K fragments
-        // are read kPfAhead steps ahead of their MFMAs through a register ring.
-        f32x4 st[4][NT];
+    // S^T tiles: s[kt][nt], lane holds keys 16kt + 4q4 + i of row 16nt + r16.
+    // Steps i = (ks, kt) run d-slice outer, key subtile inner, so consecutive
+    // MFMAs feed different accumulators; the 32 K fragments are read kPfAhead
+    // steps ahead of their MFMAs through a register ring.
+    auto compute_s = [&](auto bufc, f32x4 (&s)[4][NT]) {
+        constexpr uint32_t kOff = decltype(bufc)::value * (uint32_t)sizeof(sm.k[0]);
         bf16x8_t kf[kPfAhead];
         auto read_kfrag = [&](int i) {
             const int ks = i >> 2, kt = i & 3;
-            kf[i % kPfAhead] = as_bf16x8(lds_load16(kbuf + koff[ks & 3], 256 * (ks >> 2) + 8192 * kt));
+            kf[i % kPfAhead] = as_bf16x8(lds_load16(kaddr[ks & 3], kOff + 256 * (ks >> 2) + 8192 * kt));
         };
 #pragma unroll
         for (int i = 0; i < kPfAhead; i++) read_kfrag(i);
@@ -933,8 +965,35 @@ void prefill_mfma_kernel(PrefillArgs a) {
             if (i + kPfAhead < 32) read_kfrag(i + kPfAhead);
 #pragma unroll
             for (int nt = 0; nt < NT; nt++)
-                st[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[kt][nt], 0, 0, 0);
+                s[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[nt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[kt][nt], 0, 0, 0);
         }
+    };
+
+    // Per 64-key tile t (K(t) and V(t) in buffers t & 1): after the barrier
+    // tile t is resident and every wave is done with buffer (t + 1) & 1, which
+    // then receives tile t + 1 while tile t is computed.
+    auto step = [&](auto bufc, int t) {
+        constexpr int B = decltype(bufc)::value;
+        constexpr uint32_t kVOff = B * (uint32_t)sizeof(sm.v[0]);
+        // re-define the fragment bases here (empty asm) so base + buffer
+        // offset is not hoisted out of the loop into extra registers: the
+        // offset then folds into each read's immediate
+#pragma unroll
+        for (int j = 0; j < 4; j++) asm volatile("" : "+v"(kaddr[j]));
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) asm volatile("" : "+v"(vaddr[dt]));
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (t + 1 < n_tiles) {
+            if (2 * (t + 1) + 1 - idw0 >= 64 && 2 * (t + 1) < n_blocks) {  // uniform: next id window
+                idw0 = 2 * (t + 1);
+                idv = idw0 + lane < n_blocks ? trow[idw0 + lane] : 0;
+            }
+            issue_k(t + 1, B ^ 1);
+            issue_v(t + 1, B ^ 1);
+        }
+        f32x4 st[4][NT];
+        compute_s(PfBuf<B>{}, st);
         // pin the pipeline: kPfAhead reads, then (1 read, NT MFMAs) per step
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, kPfAhead, 0);
 #pragma unroll
@@ -942,75 +1001,77 @@ void prefill_mfma_kernel(PrefillArgs a) {
             if (i + kPfAhead < 32) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
             __builtin_amdgcn_sched_group_barrier(kSgMfma, NT, 0);
         }
-        // scale, causal mask (only on tiles that reach the diagonal or the
-        // sequence end), online softmax (lazy rescale with slack)
-        const bool full_tile = t * kPfKeys + kPfKeys - 1 <= pos0 + row0 + rw0 && t * kPfKeys + kPfKeys <= kmax;
-        bool need = false;
-        float mt[NT];
+
+        // Tile max in the log2 domain.  A full tile (all keys exist and
+        // precede the wave's first row) keeps raw scores: the max is scaled
+        // once (c >= 0 keeps the order).  A tile that reaches the diagonal or
+        // the sequence end is scaled and masked in a branch of its own (the
+        // empty asm keeps the compiler from turning it into selects on every
+        // tile), and its exponent scale is then 1.
+        const bool full = t * kPfKeys + kPfKeys - 1 <= pos0 + row0 + rw0 && t * kPfKeys + kPfKeys <= kmax;
+        if (!full) {
+            asm volatile("");
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int qpos = pos0 + row0 + rw0 + 16 * nt + r16;
-            float mx = kNegBig;
-            if (full_tile) {
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float v = st[kt][nt][i] * a.scale_log2;
-                        st[kt][nt][i] = v;
-                        mx = fmaxf(mx, v);
-                    }
-            } else {
+            for (int nt = 0; nt < NT; nt++) {
+                const int qpos = pos0 + row0 + rw0 + 16 * nt + r16;
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int kp = t * kPfKeys + 16 * kt + 4 * q4 + i;
-                        const float v = (kp <= qpos && kp < kmax) ? st[kt][nt][i] * a.scale_log2 : kNegBig;
-                        st[kt][nt][i] = v;
-                        mx = fmaxf(mx, v);
+                        st[kt][nt][i] = (kp <= qpos && kp < kmax) ? st[kt][nt][i] * c : kNegBig;
                     }
             }
+        }
+        const float cs = full ? c : 1.f;
+        bool need = false;
+        float mt[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            float mx = kNegBig;
+#pragma unroll
+            for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, st[kt][nt][i]);
             mx = max_xor16(mx);
             mx = max_xor32(mx);
-            mt[nt] = mx;
-            need |= mx > m_run[nt] + kRescaleSlack;
+            mt[nt] = full ? mx * c : mx;
+            need |= mt[nt] > m_run[nt] + kRescaleSlack;
         }
         if (__builtin_amdgcn_ballot_w64(need) != 0) {  // uniform; rows that keep their max scale by 1
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const bool up = mt[nt] > m_run[nt] + kRescaleSlack;
-                const float c = up ? fast_exp2(m_run[nt] - mt[nt]) : 1.f;
+                const float cr = up ? fast_exp2(m_run[nt] - mt[nt]) : 1.f;
                 m_run[nt] = up ? mt[nt] : m_run[nt];
-                l_lane[nt] *= c;
                 // the scaled values re-enter the accumulators through an MFMA
-                // with zero operands, which keeps O^T in the MFMA register class
+                // with zero operands, which keeps them in the MFMA register class
                 const bf16x8_t z8 = {};
 #pragma unroll
                 for (int dt = 0; dt < 16; dt++)
-                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(z8, z8, o[dt][nt] * c, 0, 0, 0);
+                    o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(z8, z8, o[dt][nt] * cr, 0, 0, 0);
+                ol[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(z8, z8, ol[nt] * cr, 0, 0, 0);
             }
         }
-        // P^T as the B operand (bf16), k-slot order (4q4 + i, 16 + 4q4 + i)
+        // P^T as the B operand (bf16), k-slot order (4q4 + i, 16 + 4q4 + i);
+        // p = 2^(s * cs - m) with one rounding before the exponential
         bf16x8_t pb_[NT][2];
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
+            const float nm = -m_run[nt];
 #pragma unroll
             for (int kk = 0; kk < 2; kk++) {
                 u32x4 w;
 #pragma unroll
-                for (int half = 0; half < 2; half++) {
-                    const f32x4 sv = st[2 * kk + half][nt];
-                    const uint32_t w0 = cvt_pk_bf16(fast_exp2(sv[0] - m_run[nt]), fast_exp2(sv[1] - m_run[nt]));
-                    const uint32_t w1 = cvt_pk_bf16(fast_exp2(sv[2] - m_run[nt]), fast_exp2(sv[3] - m_run[nt]));
-                    // the denominator sums the same rounded weights
-                    l_lane[nt] += (bf16lo(w0) + bf16hi(w0)) + (bf16lo(w1) + bf16hi(w1));
-                    w[2 * half] = w0;
-                    w[2 * half + 1] = w1;
+                for (int hf = 0; hf < 2; hf++) {
+                    const f32x4 sv = st[2 * kk + hf][nt];
+                    w[2 * hf] = cvt_pk_bf16(fast_exp2(fmaf(sv[0], cs, nm)), fast_exp2(fmaf(sv[1], cs, nm)));
+                    w[2 * hf + 1] = cvt_pk_bf16(fast_exp2(fmaf(sv[2], cs, nm)), fast_exp2(fmaf(sv[3], cs, nm)));
                 }
                 pb_[nt][kk] = as_bf16x8(w);
             }
         }
+
         // O^T += V^T . P^T; the V^T operand of lane (q4, r16) is V[keys
         // 32kk + 4q4 + e (+16)][16dt + r16]: lane J of the group addresses
         // row 32kk + 4q4 + J/4 (+16), dims 16dt + 4(J%4) .. +3
@@ -1018,8 +1079,8 @@ void prefill_mfma_kernel(PrefillArgs a) {
         bf16x8_t vf[kPfAhead];
         auto read_vfrag = [&](int i) {  // step i = (kk, dt): consecutive MFMAs feed different o[dt]
             const int kk = i >> 4, dt = i & 15;
-            const u32x2 lo = lds_load_tr16(vbuf + voff[dt], 16384 * kk);
-            const u32x2 hi = lds_load_tr16(vbuf + voff[dt], 16384 * kk + 8192);
+            const u32x2 lo = lds_load_tr16(vaddr[dt], kVOff + 16384 * kk);
+            const u32x2 hi = lds_load_tr16(vaddr[dt], kVOff + 16384 * kk + 8192);
             u32x4 w;
             w[0] = lo[0];
             w[1] = lo[1];
@@ -1038,19 +1099,30 @@ void prefill_mfma_kernel(PrefillArgs a) {
             for (int nt = 0; nt < NT; nt++)
                 o[dt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb_[nt][kk], o[dt][nt], 0, 0, 0);
         }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++)
+                ol[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb_[nt][kk], ol[nt], 0, 0, 0);
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2 * kPfAhead, 1);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             if (i + kPfAhead < 32) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 1);
             __builtin_amdgcn_sched_group_barrier(kSgMfma, NT, 1);
         }
+    };
+
+    issue_k(0, 0);
+    issue_v(0, 0);
+    for (int t = 0; t < n_tiles; t += 2) {
+        step(PfBuf<0>{}, t);
+        if (t + 1 < n_tiles) step(PfBuf<1>{}, t + 1);
     }
-    // epilogue: row sums across the 4 lane groups, normalise, gate, store
+    // epilogue: every row of a lane's ol block holds its query row's
+    // denominator; normalise, gate, store
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
-        float l = l_lane[nt];
-        l = sum_xor16(l);
-        l = sum_xor32(l);
+        const float l = ol[nt][0];
         const int rl = rw0 + 16 * nt + r16;
         if (rl >= rows) continue;
         const size_t orow = (((size_t)s * a.n_q + row0 + rl) * kQHeads + h * kGroup + g) * kHeadDim;
