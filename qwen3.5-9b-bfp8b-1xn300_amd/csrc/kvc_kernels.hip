@@ -1395,6 +1395,7 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
 constexpr int kDnThreads = 512;
 constexpr int kDnCols = 8;   // k-columns per lane (16 lanes per state row)
 constexpr int kDnRows = 8;   // state rows per lane
+constexpr int kDnBlk = 8;    // tokens per block of the chunk kernel
 
 template <bool BF16IN>
 __device__ __forceinline__ float load_f(const void* base, size_t off) {
@@ -1508,10 +1509,21 @@ template <bool BF16IN>
 __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void deltanet_kernel(DeltaNetArgs a) {
 #pragma clang fp contract(off)
-    __shared__ float conv_lds[4 * 128];  // q_kh, k_kh, v_vh0, v_vh1 (SiLU'd conv outputs)
-    __shared__ float o_lds[2][kSsmDv];   // scaled recurrence outputs of the two v-heads
-    __shared__ float4 cw_lds[kDnThreads];  // conv taps of each owned channel
-    __shared__ float4 win_lds[kDnThreads];  // conv window of each owned channel (w = unused)
+    // Tokens go in blocks of kDnBlk.  Per block:
+    //   P1 (token-parallel) thread t = owned channel: conv1d + SiLU of the
+    //      block's tokens, window in registers -> xs[tok][t];
+    //   P2 (token-parallel) 16-lane group g normalises token g's q and k in
+    //      place (dn_qk, same lanes as the one-token kernel); lanes 0..2nb-1
+    //      compute (decay, beta) of (token, v-head);
+    //   P3 (sequential) every lane updates its 8 state rows token after token
+    //      (dn_row) with no barrier inside the block -> os[tok][vl][row];
+    //   P4 (token-parallel) wave w writes the gated RMSNorm of (token,
+    //      v-head) pairs w, w + 8, ...
+    // Three barriers per block instead of two per token; the arithmetic is
+    // that of the one-token kernel, so a token gives the same bits.
+    __shared__ float xs[kDnBlk][4 * 128];        // q_kh, k_kh, v_vh0, v_vh1 of each token
+    __shared__ float2 gs[kDnBlk][2];             // (decay, beta) per token and v-head
+    __shared__ float os[kDnBlk][2][kSsmDv];      // scaled recurrence outputs
     const int b = blockIdx.x;
     const int s = b / kSsmKHeads;
     const int kh = b - s * kSsmKHeads;
@@ -1537,48 +1549,102 @@ void deltanet_kernel(DeltaNetArgs a) {
         st[r][4] = x1.x; st[r][5] = x1.y; st[r][6] = x1.z; st[r][7] = x1.w;
     }
     const int ch = dn_channel(t, kh);
-    cw_lds[t] = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch], a.conv_w[3 * kSsmC + ch]);
-    win_lds[t] = make_float4(conv[ch], conv[kSsmC + ch], conv[2 * kSsmC + ch], 0.f);
-    const float dtb = a.dt_bias[vh], av = a.a[vh];
+    const float4 cw = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch],
+                                  a.conv_w[3 * kSsmC + ch]);
+    float w0 = conv[ch], w1 = conv[kSsmC + ch], w2 = conv[2 * kSsmC + ch];  // window, oldest first
     constexpr size_t kZ = kSsmC, kAlpha = kSsmC + kSsmVHeads * kSsmDv, kBeta = kAlpha + kSsmVHeads;
-    // the next token's inputs are requested while the current one computes
-    const int zd = wi * 32 + (lane & 31);  // gated-norm dim of this lane
     const size_t prow0 = (size_t)s * a.n_tok * kSsmProj;
-    float nx = load_f<BF16IN>(a.proj, prow0 + ch);
-    float nalpha = load_f<BF16IN>(a.proj, prow0 + kAlpha + vh);
-    float nbraw = load_f<BF16IN>(a.proj, prow0 + kBeta + vh);
-    float nz = load_f<BF16IN>(a.proj, prow0 + kZ + (size_t)vh * kSsmDv + zd);
+    const int g16 = t >> 4;  // 16-lane group of P2
 
-    for (int tok = 0; tok < a.n_tok; tok++) {
-        const float x = nx, alpha = nalpha, braw = nbraw, z = nz;
-        if (tok + 1 < a.n_tok) {
-            const size_t nrow = prow0 + (size_t)(tok + 1) * kSsmProj;
-            nx = load_f<BF16IN>(a.proj, nrow + ch);
-            nalpha = load_f<BF16IN>(a.proj, nrow + kAlpha + vh);
-            nbraw = load_f<BF16IN>(a.proj, nrow + kBeta + vh);
-            nz = load_f<BF16IN>(a.proj, nrow + kZ + (size_t)vh * kSsmDv + zd);
-        }
-        const float4 cw = cw_lds[t];  // each thread reads only its own entries
-        const float4 win = win_lds[t];
-        float sum = win.x * cw.x;
-        sum = fmaf(win.y, cw.y, sum);
-        sum = fmaf(win.z, cw.z, sum);
-        sum = fmaf(x, cw.w, sum);
-        conv_lds[t] = silu_f(sum);
-        win_lds[t] = make_float4(win.y, win.z, x, 0.f);
-        __syncthreads();
-
-        float q[kDnCols], k[kDnCols], decay, beta;
-        dn_qk(conv_lds, col0, a.eps, q, k);
-        dn_gates(alpha, braw, dtb, av, decay, beta);
-        // the 16 lanes of a row hold the same output and all store it (one
-        // LDS word, same value): no branch between the rows
+    // each block's conv inputs are requested during the previous block
+    float xin[kDnBlk];
 #pragma unroll
-        for (int r = 0; r < kDnRows; r++)
-            o_lds[vl][rbase + 4 * r] =
-                dn_row(st[r], k, q, decay, beta, conv_lds[256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
+    for (int i = 0; i < kDnBlk; i++)
+        xin[i] = i < a.n_tok ? load_f<BF16IN>(a.proj, prow0 + (size_t)i * kSsmProj + ch) : 0.f;
+
+    for (int tok0 = 0; tok0 < a.n_tok; tok0 += kDnBlk) {
+        const int nb = min(kDnBlk, a.n_tok - tok0);
+        // P1: conv1d + SiLU, window pushed per token
+#pragma unroll
+        for (int i = 0; i < kDnBlk; i++) {
+            if (i < nb) {
+                const float x = xin[i];
+                float sum = w0 * cw.x;
+                sum = fmaf(w1, cw.y, sum);
+                sum = fmaf(w2, cw.z, sum);
+                sum = fmaf(x, cw.w, sum);
+                xs[i][t] = silu_f(sum);
+                w0 = w1;
+                w1 = w2;
+                w2 = x;
+            }
+        }
         __syncthreads();
-        dn_norm_out(a, o_lds[vl], lane, wi, vh, ((size_t)s * a.n_tok + tok) * (kSsmVHeads * kSsmDv), z);
+        // P2: q/k normalisation in place, gates
+        if (g16 < nb) {
+            float q[kDnCols], k[kDnCols];
+            dn_qk(xs[g16], col0, a.eps, q, k);
+#pragma unroll
+            for (int j = 0; j < kDnCols; j += 4) {
+                const int c = col0 + (j ? kSsmDk / 2 : 0);
+                *reinterpret_cast<float4*>(&xs[g16][c]) = make_float4(q[j], q[j + 1], q[j + 2], q[j + 3]);
+                *reinterpret_cast<float4*>(&xs[g16][128 + c]) = make_float4(k[j], k[j + 1], k[j + 2], k[j + 3]);
+            }
+        }
+        if (t < 2 * nb) {
+            const int gt = t >> 1, gvh = kh + kSsmKHeads * (t & 1);
+            const size_t row = prow0 + (size_t)(tok0 + gt) * kSsmProj;
+            float decay, beta;
+            dn_gates(load_f<BF16IN>(a.proj, row + kAlpha + gvh), load_f<BF16IN>(a.proj, row + kBeta + gvh),
+                     a.dt_bias[gvh], a.a[gvh], decay, beta);
+            gs[gt][t & 1] = make_float2(decay, beta);
+        }
+        __syncthreads();
+        // P3: the delta rule, token after token; the 16 lanes of a row hold
+        // the same output and all store it (one LDS word, same value)
+        for (int i = 0; i < nb; i++) {
+            float q[kDnCols], k[kDnCols];
+#pragma unroll
+            for (int j = 0; j < kDnCols; j += 4) {
+                const int c = col0 + (j ? kSsmDk / 2 : 0);
+                const float4 qq = *reinterpret_cast<const float4*>(&xs[i][c]);
+                const float4 kk = *reinterpret_cast<const float4*>(&xs[i][128 + c]);
+                q[j] = qq.x; q[j + 1] = qq.y; q[j + 2] = qq.z; q[j + 3] = qq.w;
+                k[j] = kk.x; k[j + 1] = kk.y; k[j + 2] = kk.z; k[j + 3] = kk.w;
+            }
+            const float2 gb = gs[i][vl];
+#pragma unroll
+            for (int r = 0; r < kDnRows; r++)
+                os[i][vl][rbase + 4 * r] =
+                    dn_row(st[r], k, q, gb.x, gb.y, xs[i][256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
+        }
+        __syncthreads();
+        // next block's inputs (requested here, not earlier, so that they do
+        // not hold registers through the delta-rule pass)
+        const int ntok0 = tok0 + kDnBlk;
+#pragma unroll
+        for (int i = 0; i < kDnBlk; i++)
+            if (ntok0 + i < a.n_tok) xin[i] = load_f<BF16IN>(a.proj, prow0 + (size_t)(ntok0 + i) * kSsmProj + ch);
+        // P4: gated RMSNorm of (token, v-head) pairs, all 128 dims per wave
+        for (int p = wave; p < 2 * nb; p += kDnThreads / 64) {
+            const int pt = p >> 1, pvl = p & 1, pvh = kh + kSsmKHeads * pvl;
+            const float* o_row = os[pt][pvl];
+            const float o0 = o_row[lane], o1 = o_row[lane + 64];
+            const float ss = wave_sum(fmaf(o0, o0, o1 * o1));
+            const float rms = 1.0f / sqrtf(ss / kSsmDv + a.eps);
+            const size_t row = prow0 + (size_t)(tok0 + pt) * kSsmProj;
+            const size_t out_row = ((size_t)s * a.n_tok + tok0 + pt) * (kSsmVHeads * kSsmDv) + (size_t)pvh * kSsmDv;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; h2++) {
+                const int d = lane + 64 * h2;
+                const float z = load_f<BF16IN>(a.proj, row + kZ + (size_t)pvh * kSsmDv + d);
+                const float y = o_row[d] * rms * a.norm_w[d] * silu_f(z);
+                if (a.out_bf16)
+                    static_cast<uint16_t*>(a.out)[out_row + d] = (uint16_t)f32_to_bf16_rne(y);
+                else
+                    static_cast<float*>(a.out)[out_row + d] = y;
+            }
+        }
     }
 #pragma unroll
     for (int r = 0; r < kDnRows; r++) {
@@ -1586,10 +1652,9 @@ void deltanet_kernel(DeltaNetArgs a) {
         *reinterpret_cast<float4*>(dst) = make_float4(st[r][0], st[r][1], st[r][2], st[r][3]);
         *reinterpret_cast<float4*>(dst + kSsmDk / 2) = make_float4(st[r][4], st[r][5], st[r][6], st[r][7]);
     }
-    const float4 win = win_lds[t];
-    conv[ch] = win.x;
-    conv[kSsmC + ch] = win.y;
-    conv[2 * kSsmC + ch] = win.z;
+    conv[ch] = w0;
+    conv[kSsmC + ch] = w1;
+    conv[2 * kSsmC + ch] = w2;
 }
 
 constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel
