@@ -315,3 +315,58 @@ def test_prefill_long_prefix_gate_bf16():
             ref = O.prefill_attn(q[i], mk, mv, P, n, gate=gt[i])
             O.assert_attn_close(out[i], ref, what=f"prefill P={P}")
             O.assert_attn_close(out[i], ref, rel_rms=5e-3, what=f"prefill P={P} tight")
+
+
+@pytest.mark.parametrize("scale", [-1.0 / 16, 0.0, 1.0 / 8])
+def test_attention_scale_sign_and_zero(scale):
+    """Decode and prefill take any finite softmax scale.  The prefill kernel
+    works with |scale| and moves a negative sign into Q (an exact bf16 sign
+    flip); scale 0 is uniform attention over the visible keys.  Both are
+    checked against the oracle, which applies the scale as given."""
+    say(f"attention with scale {scale}")
+    prefixes, n = [0, 300], 48
+    with make_ctx() as ctx:
+        m = Mirror(1)
+        h = kvc.hip()
+        seqs = [ctx.seq_create() for _ in prefixes]
+        for s, P in zip(seqs, prefixes):
+            if P:
+                fill_seq(ctx, m, [s], P, seed=7600 + P, layers=[0])
+        k = O.normal_bf16(len(seqs) * n * ROW, 761).reshape(len(seqs), n, ROW)
+        v = O.normal_bf16(len(seqs) * n * ROW, 762).reshape(len(seqs), n, ROW)
+        q = O.normal_bf16(len(seqs) * n * NQ * D, 763).reshape(len(seqs), n, NQ, D)
+        ctx.reserve(seqs, n)
+        kb, vb, qb = h.malloc(k.nbytes).upload(k), h.malloc(v.nbytes).upload(v), h.malloc(q.nbytes).upload(q)
+        ob = h.malloc(len(seqs) * n * NQ * D * 4)
+        ctx.append(0, seqs, n, kb, vb)
+        ctx.prefill_attn(0, seqs, n, qb, ob, scale=scale)
+        ctx.commit(seqs, n)
+        ctx.sync()
+        out = ob.download(np.float32, (len(seqs), n, NQ, D))
+        for b_ in (kb, vb, qb, ob):
+            b_.free()
+        for i, (s, P) in enumerate(zip(seqs, prefixes)):
+            m.append(s, 0, k[i], v[i])
+            mk, mv = m.get(s, 0)
+            ref = O.prefill_attn(q[i], mk, mv, P, n, scale=scale)
+            O.assert_attn_close(out[i], ref, what=f"prefill P={P} scale={scale}")
+            if scale == 0.0:  # closed form: row r averages V over keys 0 .. P + r
+                vf = O.bf16_to_f32(mv).reshape(-1, NKV, D)
+                for r in (0, n - 1):
+                    mean = vf[: P + r + 1].mean(axis=0)  # [NKV][D]
+                    want = np.repeat(mean, NQ // NKV, axis=0)
+                    O.assert_attn_close(out[i, r], want, what=f"uniform P={P} row {r}")
+        # decode on the same sequences (no new token)
+        qd = O.normal_bf16(len(seqs) * NQ * D, 764).reshape(len(seqs), NQ, D)
+        hq = kvc.hip()
+        qdb = hq.malloc(qd.nbytes).upload(qd)
+        odb = hq.malloc(len(seqs) * NQ * D * 4)
+        ctx.decode_attn(0, seqs, qdb, odb, scale=scale)
+        ctx.sync()
+        outd = odb.download(np.float32, (len(seqs), NQ, D))
+        qdb.free()
+        odb.free()
+        for i, s in enumerate(seqs):
+            mk, mv = m.get(s, 0)
+            ref = O.decode_attn(qd[i], mk, mv, prefixes[i] + n, scale=scale)
+            O.assert_attn_close(outd[i], ref, what=f"decode L={prefixes[i] + n} scale={scale}")
