@@ -721,12 +721,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // Causal chunked prefill with bf16 MFMA (v_mfma_f32_16x16x32_bf16).
 //
-// Workgroup = (sequence, kv head, 32 consecutive query positions); wave g
-// handles q head g of the GQA group, so each 64-key K/V tile staged in LDS
-// serves 4 q heads.  Per tile and wave:
-//   S^T[64 keys x 32 rows]  = K[keys x 256] . Q^T          (A = K rows, LDS)
-//   P^T = 2^(S^T - m)       (online softmax, log2 domain, bf16)
-//   O^T[256 d x 32 rows]   += V^T[d x keys] . P^T          (A = V^T, LDS)
+// Workgroup = (sequence, kv head, 32 consecutive query positions); each wave
+// handles one q head of the GQA group and 16 * NT of the 32 rows, so each
+// 64-key K/V tile staged in LDS serves 4 q heads.  Per tile and wave:
+//   S^T[64 keys x 16 NT rows]  = K[keys x 256] . Q^T       (A = K rows, LDS)
+//   P^T = 2^(S^T - m)          (online softmax, log2 domain, bf16)
+//   O^T[256 d x 16 NT rows]   += V^T[d x keys] . P^T       (A = V^T, LDS)
 // Working on transposes keeps each lane on one query row (row = lane % 16)
 // in both products, so the row statistics need no lane shuffles and P^T
 // leaves the S^T accumulator already in B-operand order.  Keys inside one
@@ -736,7 +736,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 // (global_load_lds_dwordx4, no register staging), double buffered: tile t+1
 // is in flight while tile t is computed, one barrier per tile.  Tile rows are
 // 512 B with their 16-B chunks XOR-swizzled by the row, with one pattern for
-// K and another for V (swz_k, swz_v), so that both operand reads are free of
+// K and another for V (kswz, vswz), so that both operand reads are free of
 // bank conflicts.  The V^T operand is read with ds_read_b64_tr_b16, which hands
 // lane i of each 16-lane group element i%4 of the 8-B pieces addressed by
 // lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4 -- a 4 x 16 transpose.  Rows past the
@@ -807,9 +807,9 @@ __device__ __forceinline__ u32x2 lds_load_tr16(uint32_t base, uint32_t off) {
 // SIMD, so one wave's MFMAs overlap the other's LDS reads and softmax.
 //
 // The per-tile VALU work is kept small:
-//  - full tiles are fetched with the scalar-base form of the LDS DMA, with
-//    per-lane offsets fixed at kernel start (only a tile that runs past the
-//    last key clamps rows per lane);
+//  - tiles are fetched with the scalar-base form of the LDS DMA, with
+//    per-lane offsets fixed at kernel start (a tile that runs past the last
+//    key clamps its rows per lane);
 //  - the loop is unrolled over the two buffers, so every operand-fragment
 //    address is a per-lane base plus an immediate;
 //  - scores stay unscaled on full tiles: the tile max is scaled once and the
