@@ -1404,8 +1404,28 @@ __device__ __forceinline__ float load_f(const void* base, size_t off) {
     else
         return static_cast<const float*>(base)[off];
 }
+// The same element as raw bits, widened by raw_f where it is used: an input
+// requested ahead of its use then holds no wait at the request.
+template <bool BF16IN>
+__device__ __forceinline__ uint32_t load_raw(const void* base, size_t off) {
+    if constexpr (BF16IN)
+        return static_cast<const uint16_t*>(base)[off];
+    else
+        return __float_as_uint(static_cast<const float*>(base)[off]);
+}
+template <bool BF16IN>
+__device__ __forceinline__ float raw_f(uint32_t r) {
+    return __uint_as_float(BF16IN ? r << 16 : r);
+}
 
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+// Gated-DeltaNet transcendentals on the hardware units (v_exp_f32, v_log_f32,
+// v_rcp_f32, v_rsq_f32; each within 2 ulp of the exact value, where the
+// reference uses Schraudolph's approximations).  Every DeltaNet kernel uses
+// these, so a token gives the same bits through any of them.
+__device__ __forceinline__ float dn_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float dn_log(float x) { return __builtin_amdgcn_logf(x) * 0.6931471805599453f; }
+__device__ __forceinline__ float dn_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + dn_exp(-x)); }
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
 // sum over the 16 lanes of a DPP row (every lane gets the sum)
@@ -1463,7 +1483,7 @@ __device__ __forceinline__ void dn_qk(const float* conv_lds, int col0, float eps
     }
     qn = sum16(qn);
     kn = sum16(kn);
-    const float qs = 1.0f / sqrtf(qn + eps), ks = 1.0f / sqrtf(kn + eps);
+    const float qs = dn_rsqrt(qn + eps), ks = dn_rsqrt(kn + eps);
 #pragma unroll
     for (int j = 0; j < kDnCols; j++) {
         q[j] *= qs;
@@ -1474,8 +1494,8 @@ __device__ __forceinline__ void dn_qk(const float* conv_lds, int col0, float eps
 __device__ __forceinline__ void dn_gates(float alpha, float braw, float dtb, float av, float& decay, float& beta) {
 #pragma clang fp contract(off)
     const float biased = alpha + dtb;
-    const float sp = biased > 20.0f ? biased : logf(1.0f + expf(biased));
-    decay = expf(sp * av);
+    const float sp = biased > 20.0f ? biased : dn_log(1.0f + dn_exp(biased));
+    decay = dn_exp(sp * av);
     beta = sigmoid_f(braw);
 }
 
@@ -1486,7 +1506,7 @@ __device__ __forceinline__ void dn_norm_out(const DeltaNetArgs& a, const float* 
 #pragma clang fp contract(off)
     const float o0 = o_row[lane], o1 = o_row[lane + 64];
     const float ss = wave_sum(fmaf(o0, o0, o1 * o1));
-    const float rms = 1.0f / sqrtf(ss / kSsmDv + a.eps);
+    const float rms = dn_rsqrt(ss / kSsmDv + a.eps);
     if (lane < 32) {
         const int d = wi * 32 + lane;
         const float y = o_row[d] * rms * a.norm_w[d] * silu_f(z);
@@ -1631,7 +1651,7 @@ void deltanet_kernel(DeltaNetArgs a) {
             const float* o_row = os[pt][pvl];
             const float o0 = o_row[lane], o1 = o_row[lane + 64];
             const float ss = wave_sum(fmaf(o0, o0, o1 * o1));
-            const float rms = 1.0f / sqrtf(ss / kSsmDv + a.eps);
+            const float rms = dn_rsqrt(ss / kSsmDv + a.eps);
             const size_t row = prow0 + (size_t)(tok0 + pt) * kSsmProj;
             const size_t out_row = ((size_t)s * a.n_tok + tok0 + pt) * (kSsmVHeads * kSsmDv) + (size_t)pvh * kSsmDv;
 #pragma unroll
@@ -1651,6 +1671,358 @@ void deltanet_kernel(DeltaNetArgs a) {
         float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
         *reinterpret_cast<float4*>(dst) = make_float4(st[r][0], st[r][1], st[r][2], st[r][3]);
         *reinterpret_cast<float4*>(dst + kSsmDk / 2) = make_float4(st[r][4], st[r][5], st[r][6], st[r][7]);
+    }
+    conv[ch] = w0;
+    conv[kSsmC + ch] = w1;
+    conv[2 * kSsmC + ch] = w2;
+}
+
+// ---------------------------------------------------------------------------
+// Gated-DeltaNet over chunks of 16 tokens in matrix form, on fp32 MFMA
+// (v_mfma_f32_16x16x4_f32).  Same workgroup (sequence, k-head kh, both
+// v-heads), front end (conv, q/k norms, gates) and output norm as
+// deltanet_kernel; the token loop of the delta rule is replaced by products
+// of 16-token blocks.  With a_t the decay, g_t = sum_{r<=t} log a_r (within
+// the chunk), S the state at the chunk start and U the rows
+// dd_t = beta_t (v_t - a_t S_{t-1} k_t):
+//   W1 = K S^T, W2 = Q S^T                                   [16 x 128]
+//   L  = I + diag(beta) (strict lower of e^{g_t - g_s} K K^T), T = L^-1
+//   U  = T diag(beta) (V - diag(e^g) W1)
+//   O  = diag(e^g) W2 + (lower incl. diagonal of e^{g_t - g_s} Q K^T) U
+//   S^T <- e^{g_C} S^T + Kt^T U,  Kt[s] = e^{g_C - g_s} k_s
+// which unrolls the per-token recurrence exactly (in real arithmetic); the
+// fp32 rounding differs from the token-by-token order.
+//
+// Wave w holds v-columns 32 (w % 4) .. +31 of v-head kh + 16 (w / 4): its
+// state slice is kept as MFMA B fragments, lane (g = l / 16, c = l % 16)
+// holding S^T[32 g + s][i0 + c] for s = 0..31 (the k-dim order of every
+// product is k = 32 g + s), so the state update's MFMA result lands in that
+// same layout when its A rows are taken in the order 32 (r / 4) + 4 m + r % 4.
+// Token rows of W1, U and O are taken in the order sigma(r) = 4 (r % 4) + r / 4
+// so that lane group g, register r of each of them is token 4 r + g: the
+// B fragment of a 4-token step j of the next product is then register j.
+// Tokens past the end of the last chunk enter as zero rows with beta = 0
+// and log decay 0, which leaves U, O and S unchanged.
+constexpr int kDnChunk = 16;
+
+__device__ __forceinline__ int dn_sigma(int r) { return 4 * (r & 3) + (r >> 2); }
+
+// Workgroup barrier for LDS traffic only: this wave's LDS accesses complete,
+// then s_barrier.  Unlike __syncthreads() (a release fence), it does not wait
+// for outstanding global loads, so inputs requested ahead of their use stay in
+// flight across it.  Only for kernels whose waves exchange data through LDS
+// alone.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One wave: A B for 16 x 16 row-major fp32 matrices in LDS; lane (g, c)
+// returns rows 4 g .. 4 g + 3 of column c.
+__device__ __forceinline__ f32x4 dn_m16(const float (*A)[kDnChunk], const float (*B)[kDnChunk], int g, int c) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(A[c][4 * j + g], B[4 * j + g][c], acc, 0, 0, 0);
+    return acc;
+}
+
+template <bool BF16IN>
+__global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void deltanet_mfma_kernel(DeltaNetArgs a) {
+#pragma clang fp contract(off)
+    // q_kh, k_kh (normalised), v_vh0, v_vh1 of each token; rows padded by 4
+    // floats so that lanes reading one column of 16 token rows hit 16
+    // different 4-bank groups
+    __shared__ float xs[kDnChunk][4 * 128 + 4];
+    __shared__ float lg[2][kDnChunk];          // log decay per v-head and token, then g_t
+    __shared__ float bt[2][kDnChunk];          // beta
+    __shared__ float eg[2][kDnChunk];          // e^{g_t}
+    __shared__ float fc[2][kDnChunk];          // e^{g_C - g_t}
+    __shared__ float kk[kDnChunk][kDnChunk];   // K K^T
+    __shared__ float qk[kDnChunk][kDnChunk];   // Q K^T
+    __shared__ float lm[2][kDnChunk][kDnChunk];  // strict lower of L, then T = L^-1
+    __shared__ float mm[2][kDnChunk][kDnChunk];  // e^{g_t - g_s} Q K^T, s <= t
+    __shared__ float sc[2][4][kDnChunk][kDnChunk];  // N^2, N^4, N^8 and the running product
+    __shared__ float os[kDnChunk][2][kSsmDv];    // scaled recurrence outputs
+    const int b = blockIdx.x;
+    const int s = b / kSsmKHeads;
+    const int kh = b - s * kSsmKHeads;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int hl = wave >> 2;                  // v-head of this wave's state slice
+    const int vh = kh + kSsmKHeads * hl;
+    const int g = lane >> 4, c = lane & 15;
+    const int ibase = 32 * (wave & 3);         // v-columns ibase .. +31 (two 16-column tiles)
+    const int col0 = c * 4;                    // q/k columns of the normalisation lanes
+
+    uint8_t* slot = a.state + (size_t)a.slot[s] * a.state_bytes + a.layer_off;
+    float* S = reinterpret_cast<float*>(slot) + (size_t)vh * kSsmDv * kSsmDk;
+    float* conv = reinterpret_cast<float*>(slot + a.rec_bytes);
+
+    // state slice as B fragments: st[vt][s] = S^T[32 g + s][ibase + 16 vt + c]
+    f32x4 st[2][8];
+#pragma unroll
+    for (int vt = 0; vt < 2; vt++) {
+        const float* src = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
+#pragma unroll
+        for (int m = 0; m < 8; m++) st[vt][m] = *reinterpret_cast<const f32x4*>(src + 4 * m);
+    }
+    const int ch = dn_channel(t, kh);
+    const float4 cw = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch],
+                                  a.conv_w[3 * kSsmC + ch]);
+    float w0 = conv[ch], w1 = conv[kSsmC + ch], w2 = conv[2 * kSsmC + ch];
+    constexpr size_t kZ = kSsmC, kAlpha = kSsmC + kSsmVHeads * kSsmDv, kBeta = kAlpha + kSsmVHeads;
+    const size_t prow0 = (size_t)s * a.n_tok * kSsmProj;
+    const int g16 = t >> 4;
+
+    // Inputs are requested one phase or chunk ahead of their use: a chunk's
+    // conv inputs right after the previous chunk's conv, its (alpha, beta)
+    // during the previous chunk's gate pass, its z values before the
+    // matrix pass whose output they gate.  The requests are unconditional
+    // (token index clamped to the last token; such values are not used), so
+    // that no wait is placed at a request.
+    const int last_tok = a.n_tok - 1;
+    uint32_t xin[kDnChunk];
+#pragma unroll
+    for (int i = 0; i < kDnChunk; i++)
+        xin[i] = load_raw<BF16IN>(a.proj, prow0 + (size_t)min(i, last_tok) * kSsmProj + ch);
+    // (token, v-head) of gate lane t < 32; every thread requests one pair
+    // (the others' values are not used), so no request sits in a branch
+    const int ab_t = (t >> 1) & (kDnChunk - 1), ab_vh = kh + kSsmKHeads * (t & 1);
+    uint32_t alpha_n = 0u, braw_n = 0u;
+    float dtb_g = 0.f, a_g = 0.f;
+    dtb_g = a.dt_bias[ab_vh];
+    a_g = a.a[ab_vh];
+    const float nw0 = a.norm_w[lane], nw1 = a.norm_w[lane + 64];
+    {
+        const size_t row = prow0 + (size_t)min(ab_t, last_tok) * kSsmProj;
+        alpha_n = load_raw<BF16IN>(a.proj, row + kAlpha + ab_vh);
+        braw_n = load_raw<BF16IN>(a.proj, row + kBeta + ab_vh);
+    }
+
+    for (int tok0 = 0; tok0 < a.n_tok; tok0 += kDnChunk) {
+        const int nb = min(kDnChunk, a.n_tok - tok0);
+        // P1: conv1d + SiLU (zero rows past the end)
+#pragma unroll
+        for (int i = 0; i < kDnChunk; i++) {
+            if (i < nb) {
+                const float x = raw_f<BF16IN>(xin[i]);
+                float sum = w0 * cw.x;
+                sum = fmaf(w1, cw.y, sum);
+                sum = fmaf(w2, cw.z, sum);
+                sum = fmaf(x, cw.w, sum);
+                xs[i][t] = silu_f(sum);
+                w0 = w1;
+                w1 = w2;
+                w2 = x;
+            } else {
+                xs[i][t] = 0.f;
+            }
+        }
+        lds_barrier();
+        // P2: log decay and beta (0 and 0 past the end) from the inputs
+        // requested a chunk ago, then the requests for the next chunk, then
+        // the q/k normalisation in place
+        if (t < 2 * kDnChunk) {
+            float l_a = 0.f, be = 0.f;
+            if (ab_t < nb) {
+                const float biased = raw_f<BF16IN>(alpha_n) + dtb_g;
+                const float sp = biased > 20.0f ? biased : dn_log(1.0f + dn_exp(biased));
+                l_a = sp * a_g;
+                be = sigmoid_f(raw_f<BF16IN>(braw_n));
+            }
+            lg[t & 1][ab_t] = l_a;
+            bt[t & 1][ab_t] = be;
+        }
+        {
+            const size_t row = prow0 + (size_t)min(tok0 + kDnChunk + ab_t, last_tok) * kSsmProj;
+            alpha_n = load_raw<BF16IN>(a.proj, row + kAlpha + ab_vh);
+            braw_n = load_raw<BF16IN>(a.proj, row + kBeta + ab_vh);
+        }
+        {
+            const int ntok0 = tok0 + kDnChunk;
+#pragma unroll
+            for (int i = 0; i < kDnChunk; i++)
+                xin[i] = load_raw<BF16IN>(a.proj, prow0 + (size_t)min(ntok0 + i, last_tok) * kSsmProj + ch);
+        }
+        if (g16 < nb) {
+            float q[kDnCols], k[kDnCols];
+            dn_qk(xs[g16], col0, a.eps, q, k);
+#pragma unroll
+            for (int j = 0; j < kDnCols; j += 4) {
+                const int cc = col0 + (j ? kSsmDk / 2 : 0);
+                *reinterpret_cast<float4*>(&xs[g16][cc]) = make_float4(q[j], q[j + 1], q[j + 2], q[j + 3]);
+                *reinterpret_cast<float4*>(&xs[g16][128 + cc]) = make_float4(k[j], k[j + 1], k[j + 2], k[j + 3]);
+            }
+        }
+        lds_barrier();
+        // P3a: W1 = K S^T and W2 = Q S^T for this wave's two column tiles (rows
+        // in sigma order); waves 0 and 1 also form K K^T and Q K^T; two lanes
+        // take the prefix sums of the log decays
+        f32x4 w1a[2] = {}, w2a[2] = {};
+        {
+            const float* kr = &xs[dn_sigma(c)][128 + 32 * g];
+            const float* qr = &xs[dn_sigma(c)][32 * g];
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * m);
+                const float4 q4 = *reinterpret_cast<const float4*>(qr + 4 * m);
+                const float ka[4] = {k4.x, k4.y, k4.z, k4.w}, qa[4] = {q4.x, q4.y, q4.z, q4.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int vt = 0; vt < 2; vt++) {
+                        w1a[vt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[e], st[vt][m][e], w1a[vt], 0, 0, 0);
+                        w2a[vt] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[e], st[vt][m][e], w2a[vt], 0, 0, 0);
+                    }
+            }
+        }
+        if (wave < 2) {  // wave 0: K K^T, wave 1: Q K^T (natural token order)
+            f32x4 acc = {};
+            const float* kr = &xs[c][128 + 32 * g];
+            const float* ar = wave == 0 ? kr : &xs[c][32 * g];
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * m);
+                const float4 a4 = *reinterpret_cast<const float4*>(ar + 4 * m);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, k4.x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, k4.y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, k4.z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, k4.w, acc, 0, 0, 0);
+            }
+            float(*dst)[kDnChunk] = wave == 0 ? kk : qk;
+#pragma unroll
+            for (int r = 0; r < 4; r++) dst[4 * g + r][c] = acc[r];
+        } else if (wave == 2 && lane < 2) {  // prefix sums, e^g and e^{g_C - g}
+            float run = 0.f;
+            for (int i = 0; i < kDnChunk; i++) {
+                run += lg[lane][i];
+                lg[lane][i] = run;
+                eg[lane][i] = dn_exp(run);
+            }
+            for (int i = 0; i < kDnChunk; i++) fc[lane][i] = dn_exp(run - lg[lane][i]);
+        }
+        lds_barrier();
+        // P3b: L (strict lower, beta_t e^{g_t - g_s} k_t.k_s) and the masked,
+        // decayed Q K^T; one element per thread and v-head
+        {
+            const int h = t >> 8, ti = (t >> 4) & 15, si = t & 15;
+            const float dg = dn_exp(lg[h][ti] - lg[h][si]);
+            lm[h][ti][si] = si < ti ? bt[h][ti] * (dg * kk[ti][si]) : 0.f;
+            mm[h][ti][si] = si <= ti ? dg * qk[ti][si] : 0.f;
+        }
+        lds_barrier();
+        // P3c: T = (I + N)^-1 for the strictly lower N held in lm.  N is
+        // nilpotent (N^16 = 0), so T = (I - N)(I + N^2)(I + N^4)(I + N^8)
+        // exactly: six 16 x 16 products on MFMA, one wave per v-head, through
+        // LDS (a wave's LDS accesses complete in order).
+        if (wave < 2) {
+            float(*n1)[kDnChunk] = lm[wave];
+            float(*n2)[kDnChunk] = sc[wave][0];
+            float(*n4)[kDnChunk] = sc[wave][1];
+            float(*n8)[kDnChunk] = sc[wave][2];
+            float(*x)[kDnChunk] = sc[wave][3];
+            f32x4 pr = dn_m16(n1, n1, g, c);
+#pragma unroll
+            for (int r = 0; r < 4; r++) n2[4 * g + r][c] = pr[r];
+            pr = dn_m16(n2, n2, g, c);
+#pragma unroll
+            for (int r = 0; r < 4; r++) n4[4 * g + r][c] = pr[r];
+            pr = dn_m16(n4, n4, g, c);
+#pragma unroll
+            for (int r = 0; r < 4; r++) n8[4 * g + r][c] = pr[r];
+            pr = dn_m16(n1, n2, g, c);  // X = I - N + N^2 - N N^2
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                x[4 * g + r][c] = ((4 * g + r == c) ? 1.f : 0.f) - n1[4 * g + r][c] + n2[4 * g + r][c] - pr[r];
+            pr = dn_m16(x, n4, g, c);  // X <- X + X N^4
+#pragma unroll
+            for (int r = 0; r < 4; r++) x[4 * g + r][c] += pr[r];
+            pr = dn_m16(x, n8, g, c);  // T = X + X N^8
+#pragma unroll
+            for (int r = 0; r < 4; r++) n1[4 * g + r][c] = x[4 * g + r][c] + pr[r];
+        }
+        lds_barrier();
+        // z values of this wave's output pairs (wave, wave + 8, ...) for P4
+        uint32_t zv[2 * kDnChunk / (kDnThreads / 64)][2];
+#pragma unroll
+        for (int k = 0; k < 2 * kDnChunk / (kDnThreads / 64); k++) {
+            const int p = wave + k * (kDnThreads / 64);
+            const int pt = p >> 1, pvh = kh + kSsmKHeads * (p & 1);
+            const size_t row = prow0 + (size_t)(tok0 + min(pt, nb - 1)) * kSsmProj + kZ + (size_t)pvh * kSsmDv;
+            zv[k][0] = load_raw<BF16IN>(a.proj, row + lane);
+            zv[k][1] = load_raw<BF16IN>(a.proj, row + lane + 64);
+        }
+        // P3d: U = T diag(beta) (V - diag(e^g) W1); O = diag(e^g) W2 + M U;
+        // S^T <- e^{g_C} S^T + Kt^T U.  Lane group g, register r <-> token 4 r + g.
+        const float egc = eg[hl][kDnChunk - 1];
+        f32x4 u[2];
+#pragma unroll
+        for (int vt = 0; vt < 2; vt++) {
+            const int i = ibase + 16 * vt + c;
+            f32x4 rhs;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tau = 4 * r + g;
+                rhs[r] = bt[hl][tau] * (xs[tau][256 + 128 * hl + i] - eg[hl][tau] * w1a[vt][r]);
+            }
+            f32x4 acc = {};
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(lm[hl][dn_sigma(c)][4 * j + g], rhs[j], acc, 0, 0, 0);
+            u[vt] = acc;
+            f32x4 o;
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[r] = eg[hl][4 * r + g] * w2a[vt][r];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                o = __builtin_amdgcn_mfma_f32_16x16x4f32(mm[hl][dn_sigma(c)][4 * j + g], u[vt][j], o, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) os[4 * r + g][hl][i] = o[r] * a.out_scale;
+        }
+#pragma unroll
+        for (int vt = 0; vt < 2; vt++)
+#pragma unroll
+            for (int m = 0; m < 8; m++) st[vt][m] *= egc;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tok = 4 * j + g;
+            const float f = fc[hl][tok];
+#pragma unroll
+            for (int m = 0; m < 8; m++) {
+                const float ak = f * xs[tok][128 + 32 * (c >> 2) + 4 * m + (c & 3)];
+#pragma unroll
+                for (int vt = 0; vt < 2; vt++)
+                    st[vt][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak, u[vt][j], st[vt][m], 0, 0, 0);
+            }
+        }
+        lds_barrier();
+        // P4: gated RMSNorm of (token, v-head) pairs, all 128 dims per wave
+#pragma unroll
+        for (int k = 0; k < 2 * kDnChunk / (kDnThreads / 64); k++) {
+            const int p = wave + k * (kDnThreads / 64);
+            if (p >= 2 * nb) break;
+            const int pt = p >> 1, pvl = p & 1, pvh = kh + kSsmKHeads * pvl;
+            const float* o_row = os[pt][pvl];
+            const float o0 = o_row[lane], o1 = o_row[lane + 64];
+            const float ss = wave_sum(fmaf(o0, o0, o1 * o1));
+            const float rms = dn_rsqrt(ss / kSsmDv + a.eps);
+            const size_t out_row = ((size_t)s * a.n_tok + tok0 + pt) * (kSsmVHeads * kSsmDv) + (size_t)pvh * kSsmDv;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; h2++) {
+                const int d = lane + 64 * h2;
+                const float y = o_row[d] * rms * (h2 ? nw1 : nw0) * silu_f(raw_f<BF16IN>(zv[k][h2]));
+                if (a.out_bf16)
+                    static_cast<uint16_t*>(a.out)[out_row + d] = (uint16_t)f32_to_bf16_rne(y);
+                else
+                    static_cast<float*>(a.out)[out_row + d] = y;
+            }
+        }
+    }
+#pragma unroll
+    for (int vt = 0; vt < 2; vt++) {
+        float* dst = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
+#pragma unroll
+        for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 4 * m) = st[vt][m];
     }
     conv[ch] = w0;
     conv[kSsmC + ch] = w1;
@@ -1922,6 +2294,11 @@ int launch_deltanet(const DeltaNetArgs& a, void* stream) {
             hipLaunchKernelGGL(deltanet_decode_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
         else
             hipLaunchKernelGGL(deltanet_decode_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
+    } else if (a.n_tok >= kDnChunk) {
+        if (a.in_bf16)
+            hipLaunchKernelGGL(deltanet_mfma_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(deltanet_mfma_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
     } else if (a.in_bf16) {
         hipLaunchKernelGGL(deltanet_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
     } else {

@@ -241,3 +241,55 @@ def test_deltanet_state_is_zero_after_create_and_reset():
         assert is_zero(s2)  # kvc_state_ptrs finishes the fill before returning
     for b_ in bufs + [ob]:
         b_.free()
+
+
+@pytest.mark.parametrize("n_tok", [16, 37, 128])
+def test_deltanet_matrix_form_chunks_match_oracle(n_tok):
+    """Calls of 16 or more tokens take the matrix (WY) form over 16-token
+    blocks on fp32 MFMA; 37 tokens end in a partial block.  Every token's
+    output and the final state are held to the same fp32 bar as the
+    token-by-token kernels."""
+    say(f"deltanet matrix form, {n_tok} tokens")
+    run_case(kvc.DTYPE_BF16, kvc.DTYPE_F32, n_tok=n_tok, n_seqs=2, seed=7700 + n_tok)
+
+
+def test_deltanet_matrix_form_bf16_out():
+    say("deltanet matrix form, fp32 in, bf16 out")
+    run_case(kvc.DTYPE_F32, kvc.DTYPE_BF16, n_tok=33, n_seqs=1, seed=7800)
+
+
+def test_deltanet_matrix_form_equals_token_steps_after_restore():
+    """From a restored snapshot, one 32-token call (matrix form) and 32
+    one-token calls give the same outputs and state to the fp32 bar."""
+    say("deltanet matrix form vs token steps after restore")
+    h = kvc.hip()
+    rng = np.random.default_rng(7900)
+    conv_w, dtb, a, nw = weights(7901)
+    n = 32
+    with ctx_ssm() as ctx:
+        s = ctx.seq_create()
+        fill_seq(ctx, Mirror(1), [s], 256, seed=7902)
+        rb, cb = state_bufs(ctx, s, 1)
+        rb.upload((0.05 * rng.standard_normal((NV, DV, DK))).astype(np.float32))
+        cb.upload(rng.standard_normal((3, C)).astype(np.float32))
+        proj = O.f32_to_bf16(rng.standard_normal((n, PROJ)).astype(np.float32))
+        bufs = [kvc.to_device(x_) for x_ in (proj, conv_w, dtb, a, nw)]
+        ob = h.malloc(n * NV * DV * 4)
+        ids = ctx.snapshot_save([s])
+        for t in range(n):
+            ctx.deltanet_step(1, [s], 1, bufs[0].ptr + t * PROJ * 2, bufs[1], bufs[2], bufs[3], bufs[4],
+                              ob.ptr + t * NV * DV * 4)
+        ctx.sync()
+        steps = ob.download(np.float32, (n, NV * DV))
+        r_steps = rb.download(np.float32, (NV, DV, DK))
+        ctx.snapshot_restore([s], ids)
+        ctx.deltanet_step(1, [s], n, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], ob)
+        ctx.sync()
+        chunk = ob.download(np.float32, (n, NV * DV))
+        r_chunk = rb.download(np.float32, (NV, DV, DK))
+        ctx.snapshot_release(ids[0])
+        for b_ in bufs + [ob]:
+            b_.free()
+    for t in range(n):
+        rel_close(chunk[t], steps[t], f"token {t}")
+    rel_close(r_chunk, r_steps, "state after 32 tokens")
