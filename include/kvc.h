@@ -228,10 +228,12 @@ int kvc_state_ptrs(kvc_ctx* ctx, int32_t seq, int32_t ssm_layer, void** rec,
  * first, tap 3 on the input), dt_bias [v_heads], a [v_heads] (decay =
  * exp(softplus(alpha + dt_bias) * a)), norm_w [v_dim].  out: [n_seqs][n_tok]
  * [v_heads * v_dim], fp32 or bf16 (RNE) by out_dtype: the gated-RMSNorm
- * output (o / rms(o) * norm_w * silu(z), o = S q / 11.3137).  exp, sigmoid and
- * SiLU are exact where the reference uses Schraudolph approximations
- * (:2349-2374).  Built for 32 v-heads, 16 k-heads, 128 x 128 heads, a 3-row
- * window and 8192 channels (KVC_ERR_UNSUPPORTED otherwise). */
+ * output (o / rms(o) * norm_w * silu(z), o = S q / 11.3137).  exp, log,
+ * sigmoid and SiLU use the hardware exp2/log2/reciprocal (each within 2 ulp)
+ * where the reference uses Schraudolph approximations (:2349-2374).  Built for
+ * 32 v-heads, 16 k-heads, 128 x 128 heads, a 3-row window and 8192 channels
+ * (KVC_ERR_UNSUPPORTED otherwise); one seq's n_tok rows of proj must span
+ * less than 2 GiB (KVC_ERR_RANGE otherwise). */
 int kvc_deltanet_step(kvc_ctx* ctx, int32_t ssm_layer, const int32_t* seqs,
                       int32_t n_seqs, int32_t n_tok, const void* proj,
                       int32_t in_dtype, const void* conv_w, const void* dt_bias,

@@ -1246,6 +1246,9 @@ int kvc_deltanet_step(kvc_ctx* c, int32_t ssm_layer, const int32_t* seqs, int32_
         (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16))
         return set_err(KVC_ERR_INVALID, "bad in_dtype / out_dtype");
     const size_t isz = in_dtype == KVC_DTYPE_BF16 ? 2 : 4, osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
+    // the chunk kernel addresses one seq's rows with 32-bit buffer offsets
+    if ((size_t)n_tok * kSsmProj * isz >= ((size_t)1 << 31))
+        return set_err(KVC_ERR_RANGE, "n_tok %d: one seq's projection rows exceed 2 GiB", n_tok);
     if ((rc = clean_states(c, seqs, (size_t)n_seqs, stream))) return rc;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
         const int32_t n = std::min(kMaxBatch, n_seqs - i0);

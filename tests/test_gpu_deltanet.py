@@ -293,3 +293,28 @@ def test_deltanet_matrix_form_equals_token_steps_after_restore():
     for t in range(n):
         rel_close(chunk[t], steps[t], f"token {t}")
     rel_close(r_chunk, r_steps, "state after 32 tokens")
+
+
+@pytest.mark.parametrize("in_dtype,n_tok", [(kvc.DTYPE_BF16, (1 << 31) // (PROJ * 2) + 1),
+                                            (kvc.DTYPE_F32, (1 << 31) // (PROJ * 4) + 1)])
+def test_deltanet_rejects_rows_past_2gib(in_dtype, n_tok):
+    """The chunk kernel addresses one sequence's projection rows with 32-bit
+    buffer offsets: a call whose rows span 2 GiB or more is refused with
+    KVC_ERR_RANGE before anything is launched (the buffers are never read),
+    and the context stays usable."""
+    say(f"deltanet n_tok={n_tok} rejected")
+    h = kvc.hip()
+    conv_w, dtb, a, nw = weights(7600)
+    bufs = [kvc.to_device(x_) for x_ in (np.zeros(PROJ, np.float32), conv_w, dtb, a, nw)]
+    ob = h.malloc(NV * DV * 4)
+    with ctx_ssm() as ctx:
+        s = ctx.seq_create()
+        with pytest.raises(kvc.KvcError) as e:
+            ctx.deltanet_step(1, [s], n_tok, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], ob, in_dtype=in_dtype)
+        assert e.value.code == kvc.KVC_ERR_RANGE
+        # one token still runs
+        ctx.deltanet_step(1, [s], 1, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], ob, in_dtype=kvc.DTYPE_F32)
+        ctx.sync()
+        assert np.isfinite(ob.download(np.float32, (NV * DV,))).all()
+    for b_ in bufs + [ob]:
+        b_.free()
