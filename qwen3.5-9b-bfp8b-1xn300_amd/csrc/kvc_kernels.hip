@@ -1535,6 +1535,21 @@ __device__ __forceinline__ int dn_channel(int t, int kh) {
                        : 2 * kSsmKHeads * kSsmDk + (kh + kSsmKHeads * (part - 2)) * kSsmDv + ci;
 }
 
+// Streaming access to the recurrent state for the kernels whose wave
+// instructions each cover whole 256-B row pieces: each element is read once
+// and written once per step, so the loads and stores are non-temporal (no
+// cache allocation for data that will not be reused before it is evicted).
+// Measured on the one-token step: 58.9 -> 51.1 us per layer at config e, most
+// of it from the stores.  The matrix-form kernel's slices are 16-B pieces
+// 128 B apart per instruction; there non-temporal access was slower.
+__device__ __forceinline__ float4 nt_ld4(const float* p) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void nt_st4(float* p, float x, float y, float z, float w) {
+    __builtin_nontemporal_store(f32x4{x, y, z, w}, reinterpret_cast<f32x4*>(p));
+}
+
 template <bool BF16IN>
 __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void deltanet_kernel(DeltaNetArgs a) {
@@ -1573,8 +1588,8 @@ void deltanet_kernel(DeltaNetArgs a) {
 #pragma unroll
     for (int r = 0; r < kDnRows; r++) {
         const float* src = S + (size_t)(rbase + 4 * r) * kSsmDk;
-        const float4 x0 = *reinterpret_cast<const float4*>(src);
-        const float4 x1 = *reinterpret_cast<const float4*>(src + kSsmDk / 2);
+        const float4 x0 = nt_ld4(src);
+        const float4 x1 = nt_ld4(src + kSsmDk / 2);
         st[r][0] = x0.x; st[r][1] = x0.y; st[r][2] = x0.z; st[r][3] = x0.w;
         st[r][4] = x1.x; st[r][5] = x1.y; st[r][6] = x1.z; st[r][7] = x1.w;
     }
@@ -1679,8 +1694,8 @@ void deltanet_kernel(DeltaNetArgs a) {
 #pragma unroll
     for (int r = 0; r < kDnRows; r++) {
         float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
-        *reinterpret_cast<float4*>(dst) = make_float4(st[r][0], st[r][1], st[r][2], st[r][3]);
-        *reinterpret_cast<float4*>(dst + kSsmDk / 2) = make_float4(st[r][4], st[r][5], st[r][6], st[r][7]);
+        nt_st4(dst, st[r][0], st[r][1], st[r][2], st[r][3]);
+        nt_st4(dst + kSsmDk / 2, st[r][4], st[r][5], st[r][6], st[r][7]);
     }
     conv[ch] = w0;
     conv[kSsmC + ch] = w1;
@@ -2164,8 +2179,8 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArg
 #pragma unroll
     for (int p = 0; p < kDnPf; p++) {
         const float* src = S + (size_t)(rbase + 4 * p) * kSsmDk;
-        buf[p][0] = *reinterpret_cast<const float4*>(src);
-        buf[p][1] = *reinterpret_cast<const float4*>(src + kSsmDk / 2);
+        buf[p][0] = nt_ld4(src);
+        buf[p][1] = nt_ld4(src + kSsmDk / 2);
     }
     const int ch = dn_channel(t, kh);
     const size_t prow = (size_t)s * kSsmProj;
@@ -2195,13 +2210,13 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArg
                              buf[r % kDnPf][1].x, buf[r % kDnPf][1].y, buf[r % kDnPf][1].z, buf[r % kDnPf][1].w};
         if (r + kDnPf < kDnRows) {
             const float* src = S + (size_t)(rbase + 4 * (r + kDnPf)) * kSsmDk;
-            buf[r % kDnPf][0] = *reinterpret_cast<const float4*>(src);
-            buf[r % kDnPf][1] = *reinterpret_cast<const float4*>(src + kSsmDk / 2);
+            buf[r % kDnPf][0] = nt_ld4(src);
+            buf[r % kDnPf][1] = nt_ld4(src + kSsmDk / 2);
         }
         o_lds[vl][rbase + 4 * r] = dn_row(st, k, q, decay, beta, conv_lds[256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
         float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
-        *reinterpret_cast<float4*>(dst) = make_float4(st[0], st[1], st[2], st[3]);
-        *reinterpret_cast<float4*>(dst + kSsmDk / 2) = make_float4(st[4], st[5], st[6], st[7]);
+        nt_st4(dst, st[0], st[1], st[2], st[3]);
+        nt_st4(dst + kSsmDk / 2, st[4], st[5], st[6], st[7]);
     }
     __syncthreads();
     dn_norm_out(a, o_lds[vl], lane, wi, vh, (size_t)s * (kSsmVHeads * kSsmDv), z);
