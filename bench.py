@@ -385,6 +385,7 @@ def cpu_baseline_e(n_sessions=64):
     return {"kind": "port", "cores": cores,
             "snapshot_GBps_1thread": round(2 * 4 * per_sess / c_s / 1e9, 2),
             "resume_decode_us_per_layer": round(d_s * n_sessions / cores * 1e6, 1),
+            "resume_short8_us_per_layer": round(chunk_us * 8 / 128, 1),
             "resume_chunk128_us_per_layer": round(chunk_us, 1),
             "resume_chunk128_TFLOPs": round(n_sessions * 128 * DN_TOKEN_FLOP / (chunk_us * 1e-6) / 1e12, 5),
             "sample": f"4 session snapshots copied (1 thread); the oracle's Gated-DeltaNet step of one layer for "
@@ -650,7 +651,8 @@ def run_e(args):
                         for l_ in range(n_ssm)]
 
     dn_us = {}
-    for name, n_tok, n_rep in (("decode", 1, 20), ("chunk", n_chunk, 2)):
+    n_short = 8  # a short call (a few tokens, e.g. a verify step) takes the blocked sequential kernel
+    for name, n_tok, n_rep in (("decode", 1, 20), ("short", n_short, 10), ("chunk", n_chunk, 2)):
         g_ = h.capture(stream, dn_leg(n_tok))
         h.graph_launch(g_, stream)  # warm-up
         h.record(e0, stream)
@@ -662,6 +664,7 @@ def run_e(args):
     layer_state = rec_b + conv_b
     dec_bytes = nses * (2 * layer_state + proj_row * 2 + out_row * 2)
     chunk_bytes = nses * (2 * layer_state + n_chunk * (proj_row * 2 + out_row * 2))
+    short_bytes = nses * (2 * layer_state + n_short * (proj_row * 2 + out_row * 2))
     # delta rule per token and layer: 32 v-heads x 128 x 128 state x (decay mul + 3 FMA)
     chunk_flops = nses * n_chunk * cf.ssm_v_heads * cf.ssm_v_dim * cf.ssm_k_dim * 7
     for b_ in wts + [proj, dn_out]:
@@ -669,12 +672,14 @@ def run_e(args):
     ctx.close()
     return {"workload": "e: 24 Gated-DeltaNet + 8 attention layers, 64 sessions, save then restore at a 256-token "
                         "boundary (fp32 recurrent + conv state, bf16 K/V of the segment), then resume: the 24 "
-                        "Gated-DeltaNet layers on the restored state for one decode token and for a 128-token "
-                        "chunk (bf16 projection rows in, bf16 out)",
+                        "Gated-DeltaNet layers on the restored state for one decode token, for an 8-token call "
+                        "and for a 128-token chunk (bf16 projection rows in, bf16 out)",
             "bytes_per_session": per_sess, "save_ms": round(sv_ms, 3), "restore_ms": round(rs_ms, 3),
             "save_GBps": round(moved / (sv_ms * 1e-3) / 1e9, 1), "restore_GBps": round(moved / (rs_ms * 1e-3) / 1e9, 1),
             "resume_decode_us_per_layer": round(dn_us["decode"], 1),
             "resume_decode_GBps": round(dec_bytes / (dn_us["decode"] * 1e-6) / 1e9, 1),
+            "resume_short8_us_per_layer": round(dn_us["short"], 1),
+            "resume_short8_GBps": round(short_bytes / (dn_us["short"] * 1e-6) / 1e9, 1),
             "resume_chunk128_us_per_layer": round(dn_us["chunk"], 1),
             "resume_chunk128_GBps": round(chunk_bytes / (dn_us["chunk"] * 1e-6) / 1e9, 1),
             "resume_chunk128_TFLOPs": round(chunk_flops / (dn_us["chunk"] * 1e-6) / 1e12, 2),
