@@ -1766,7 +1766,10 @@ __device__ __forceinline__ f32x4 dn_m16(const float (*A)[kDnChunk], const float 
 // overlaps the state waves' MFMAs.  Their VALU work does not: measured phase
 // times come out as the SIMD's MFMA time plus the helpers' VALU time.
 // Per-block LDS data are triple buffered (token rows, gate data: written two
-// blocks ahead) or double buffered (outputs).
+// blocks ahead) or double buffered (outputs).  The kernel is persistent (one
+// workgroup per CU, items taken in turn), so "block b" is a position in the
+// workgroup's stream of blocks over its items; the two-block pipeline fill
+// happens once per workgroup, not once per item.
 constexpr int kDnMathWaves = 8;
 constexpr int kDnHelpWaves = 8;
 constexpr int kDnMfmaThreads = 64 * (kDnMathWaves + kDnHelpWaves);
@@ -1789,15 +1792,23 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
     __shared__ float mm[2][kDnChunk][kDnChunk];   // e^{g_t - g_s} Q K^T, s <= t
     __shared__ float sc[2][4][kDnChunk][kDnChunk];  // N^2, N^4, N^8 and the running product
     __shared__ float os[2][kDnChunk][2][kSsmDv];  // scaled recurrence outputs
-    const int b = blockIdx.x;
-    const int s = b / kSsmKHeads;
-    const int kh = b - s * kSsmKHeads;
+    // Persistent: workgroup w runs items (sequence, k-head) w, w + G, ...
+    // (G = grid size) as one stream of blocks; position q of the stream is
+    // block q % nblk of item w + (q / nblk) G.  The helpers' pipeline runs
+    // across item boundaries, and a state wave's switch to the next item is
+    // one store and one load of its slice.
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int g = lane >> 4, c = lane & 15;
-    uint8_t* slot = a.state + (size_t)a.slot[s] * a.state_bytes + a.layer_off;
     const int nblk = (a.n_tok + kDnChunk - 1) / kDnChunk;
+    const int n_items = a.n_seqs * kSsmKHeads;
+    const int n_my = ((int)(n_items - blockIdx.x) + (int)gridDim.x - 1) / (int)gridDim.x;  // >= 1
+    const int n_pos = n_my * nblk;
+    auto item_at = [&](int q) { return (int)blockIdx.x + (max(min(q, n_pos - 1), 0) / nblk) * (int)gridDim.x; };
+    auto slot_of = [&](int item) {
+        return a.state + (size_t)a.slot[item / kSsmKHeads] * a.state_bytes + a.layer_off;
+    };
 
     // The state waves and the helper waves run separate loops with the same
     // number of barriers (two per iteration), so that neither holds the
@@ -1807,19 +1818,36 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
         // slice as B fragments: st[vt][m] = S^T[32 g + 4 m .. +3][ibase + 16 vt + c]
         const int hl = wave >> 2;
         const int ibase = 32 * (wave & 3);
-        float* S = reinterpret_cast<float*>(slot) + (size_t)(kh + kSsmKHeads * hl) * kSsmDv * kSsmDk;
+        auto slice_of = [&](int item) {
+            return reinterpret_cast<float*>(slot_of(item)) + (size_t)(item % kSsmKHeads + kSsmKHeads * hl) * kSsmDv * kSsmDk;
+        };
         f32x4 st[2][8];
+        auto load_state = [&](const float* S) {
 #pragma unroll
-        for (int vt = 0; vt < 2; vt++) {
-            const float* src = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
+            for (int vt = 0; vt < 2; vt++) {
+                const float* src = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
 #pragma unroll
-            for (int m = 0; m < 8; m++) st[vt][m] = *reinterpret_cast<const f32x4*>(src + 4 * m);
-        }
-        lds_barrier();  // iteration -2
+                for (int m = 0; m < 8; m++) st[vt][m] = *reinterpret_cast<const f32x4*>(src + 4 * m);
+            }
+        };
+        auto store_state = [&](float* S) {
+#pragma unroll
+            for (int vt = 0; vt < 2; vt++) {
+                float* dst = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
+#pragma unroll
+                for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 4 * m) = st[vt][m];
+            }
+        };
+        load_state(slice_of(item_at(0)));
+        lds_barrier();  // positions -2, -1
         lds_barrier();
-        lds_barrier();  // iteration -1
         lds_barrier();
-        for (int bb = 0; bb < nblk; bb++) {
+        lds_barrier();
+        for (int bb = 0; bb < n_pos; bb++) {
+            if (bb > 0 && bb % nblk == 0) {  // next item: this slice out, the next one in
+                store_state(slice_of(item_at(bb - 1)));
+                load_state(slice_of(item_at(bb)));
+            }
             const int cur = bb % 3;
             const float(*x)[4 * 128 + 4] = xs[cur];
             // Phase A: W1 = K S^T and W2 = Q S^T (rows in sigma order)
@@ -1887,81 +1915,105 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             }
             lds_barrier();
         }
-#pragma unroll
-        for (int vt = 0; vt < 2; vt++) {
-            float* dst = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
-#pragma unroll
-            for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 4 * m) = st[vt][m];
-        }
+        store_state(slice_of(item_at(n_pos - 1)));
         return;
     }
 
-    // ---- helper waves: thread u owns conv channel u (and xs column u) ----
+    // ---- helper waves: thread u owns conv channel u (and xs column u) of
+    // the current item ----
     // The helpers issue ahead of the state waves on their SIMD (wave
     // priority 2 against 0): their phase work is a latency chain, and with
     // equal priority the older state waves' MFMA streams delay it.
     __builtin_amdgcn_s_setprio(2);
-    float* conv = reinterpret_cast<float*>(slot + a.rec_bytes);
     constexpr size_t kZ = kSsmC, kAlpha = kSsmC + kSsmVHeads * kSsmDv, kBeta = kAlpha + kSsmVHeads;
-    const size_t prow0 = (size_t)s * a.n_tok * kSsmProj;
     const int last_tok = a.n_tok - 1;
     const int u = t - 64 * kDnMathWaves;
     const int hw = wave - kDnMathWaves;
-    // Buffer resources over this sequence's projection rows (the launch
+    // Buffer resources over one sequence's projection rows (the launch
     // checks that they span less than 2 GiB) and outputs.  Loads take the
     // row's byte offset in an SGPR and the element's in a VGPR, with token
     // indices clamped to the sequence; a store whose offset is past the end
     // (kDrop) is discarded by the hardware, so every output pair is stored
     // unconditionally.
     constexpr uint32_t kElt = BF16IN ? 2u : 4u;
-    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(static_cast<const char*>(a.proj) + prow0 * kElt), 0,
-        (int)((uint32_t)a.n_tok * (uint32_t)kSsmProj * kElt), 0x00020000);
-    auto row_off = [&](int tok) { return (uint32_t)max(min(tok, last_tok), 0) * (uint32_t)kSsmProj * kElt; };
     constexpr uint32_t osz = BF16OUT ? 2u : 4u;
-    const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
-        static_cast<char*>(a.out) + (size_t)s * a.n_tok * (kSsmVHeads * kSsmDv) * osz, 0,
-        (int)((uint32_t)a.n_tok * (uint32_t)(kSsmVHeads * kSsmDv) * osz), 0x00020000);
+    auto proj_rs = [&](int seq) {
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<char*>(static_cast<const char*>(a.proj) + (size_t)seq * a.n_tok * kSsmProj * kElt), 0,
+            (int)((uint32_t)a.n_tok * (uint32_t)kSsmProj * kElt), 0x00020000);
+    };
+    auto out_rs = [&](int seq) {
+        return __builtin_amdgcn_make_buffer_rsrc(
+            static_cast<char*>(a.out) + (size_t)seq * a.n_tok * (kSsmVHeads * kSsmDv) * osz, 0,
+            (int)((uint32_t)a.n_tok * (uint32_t)(kSsmVHeads * kSsmDv) * osz), 0x00020000);
+    };
+    auto row_off = [&](int tok) { return (uint32_t)max(min(tok, last_tok), 0) * (uint32_t)kSsmProj * kElt; };
     constexpr uint32_t kDrop = 0xFFFFFF00u;
-    const int ch = dn_channel(u, kh);
-    const uint32_t ch_off = (uint32_t)ch * kElt;
-    const float4 cw = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch],
-                                  a.conv_w[3 * kSsmC + ch]);
-    float w0 = conv[ch], w1 = conv[kSsmC + ch], w2 = conv[2 * kSsmC + ch];
-    // gate pair (token ab_t, v-head ab_vh) of lane u % 32 (helper 3's lanes
-    // 0..31 compute theirs); norm lanes: helpers 4..7, token g16, columns of c
-    const int ab_t = (u >> 1) & (kDnChunk - 1), ab_vh = kh + kSsmKHeads * (u & 1);
-    const float dtb_g = a.dt_bias[ab_vh], a_g = a.a[ab_vh];
+    // gate pair (token ab_t, v-head offset ab_h) of lane u % 32 (helper 3's
+    // lanes 0..31 compute theirs); norm lanes: helpers 4..7, token g16,
+    // columns of c
+    const int ab_t = (u >> 1) & (kDnChunk - 1), ab_h = u & 1;
     const float nw0 = a.norm_w[lane], nw1 = a.norm_w[lane + 64];
     const int g16 = (u - 256) >> 4, col0 = c * 4;
     constexpr int kPairs = 2 * kDnChunk / kDnHelpWaves;  // output pairs per helper wave
 
-    // Requests: conv inputs, alpha and beta of a block; z values of a block.
-    // Each is issued unconditionally and marked used (use_x, use_z) at a
-    // fixed point of a later phase, so that the waits the compiler places
-    // there are the same on every path and cover only requests at least a
-    // phase old.
+    // conv channel, weights and window of the item whose conv runs next
+    int cv_item = -1;
+    float* conv = nullptr;
+    int ch = 0;
+    float4 cw = {};
+    float w0 = 0.f, w1 = 0.f, w2 = 0.f, dtb_g = 0.f, a_g = 0.f;
+    auto conv_item = [&](int item) {
+        conv = reinterpret_cast<float*>(slot_of(item) + a.rec_bytes);
+        const int kh = item % kSsmKHeads;
+        ch = dn_channel(u, kh);
+        cw = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch], a.conv_w[3 * kSsmC + ch]);
+        w0 = conv[ch];
+        w1 = conv[kSsmC + ch];
+        w2 = conv[2 * kSsmC + ch];
+        dtb_g = a.dt_bias[kh + kSsmKHeads * ab_h];
+        a_g = a.a[kh + kSsmKHeads * ab_h];
+    };
+    auto conv_done = [&] {
+        conv[ch] = w0;
+        conv[kSsmC + ch] = w1;
+        conv[2 * kSsmC + ch] = w2;
+    };
+
+    // Requests: conv inputs, alpha and beta of a stream position; z values
+    // of a position.  Each is issued unconditionally (positions and token
+    // indices clamped) and marked used (use_x, use_z) at a fixed point of a
+    // later phase, so that the waits the compiler places there are the same
+    // on every path and cover only requests at least a phase old.
     uint32_t xin[kDnChunk], alpha_n, braw_n, zv[kPairs][2];
-    auto request_x = [&](int bb) {
+    auto request_x = [&](int q) {
+        const int item = item_at(q), kh = item % kSsmKHeads;
+        const int tb = (max(min(q, n_pos - 1), 0) % nblk) * kDnChunk;
+        const __amdgpu_buffer_rsrc_t prs = proj_rs(item / kSsmKHeads);
+        const uint32_t ch_off = (uint32_t)dn_channel(u, kh) * kElt;
 #pragma unroll
-        for (int i = 0; i < kDnChunk; i++) xin[i] = load_raw_buf<BF16IN>(prs, ch_off, row_off(bb * kDnChunk + i));
-        const int tb = max(min(bb * kDnChunk, last_tok), 0);
-        const uint32_t ro = row_off(tb);
-        const uint32_t lt = (uint32_t)min(ab_t, last_tok - tb) * (uint32_t)kSsmProj * kElt;
-        alpha_n = load_raw_buf<BF16IN>(prs, lt + (uint32_t)(kAlpha + ab_vh) * kElt, ro);
-        braw_n = load_raw_buf<BF16IN>(prs, lt + (uint32_t)(kBeta + ab_vh) * kElt, ro);
+        for (int i = 0; i < kDnChunk; i++) xin[i] = load_raw_buf<BF16IN>(prs, ch_off, row_off(tb + i));
+        const int tr = min(tb, last_tok);
+        const uint32_t ro = row_off(tr);
+        const uint32_t lt = (uint32_t)min(ab_t, last_tok - tr) * (uint32_t)kSsmProj * kElt;
+        const int vh = kh + kSsmKHeads * ab_h;
+        alpha_n = load_raw_buf<BF16IN>(prs, lt + (uint32_t)(kAlpha + vh) * kElt, ro);
+        braw_n = load_raw_buf<BF16IN>(prs, lt + (uint32_t)(kBeta + vh) * kElt, ro);
     };
     auto use_x = [&] {
 #pragma unroll
         for (int i = 0; i < kDnChunk; i++) asm volatile("" ::"v"(xin[i]));
         asm volatile("" ::"v"(alpha_n), "v"(braw_n));
     };
-    auto request_z = [&](int bb) {
+    auto request_z = [&](int q) {
+        const int item = item_at(q), kh = item % kSsmKHeads;
+        const int tb = (max(min(q, n_pos - 1), 0) % nblk) * kDnChunk;
+        const __amdgpu_buffer_rsrc_t prs = proj_rs(item / kSsmKHeads);
 #pragma unroll
         for (int k = 0; k < kPairs; k++) {
             const int p = hw + k * kDnHelpWaves;
             const int pt = p >> 1, pvh = kh + kSsmKHeads * (p & 1);
-            const uint32_t ro = row_off(bb * kDnChunk + pt), lo = (uint32_t)(kZ + pvh * kSsmDv + lane) * kElt;
+            const uint32_t ro = row_off(tb + pt), lo = (uint32_t)(kZ + pvh * kSsmDv + lane) * kElt;
             zv[k][0] = load_raw_buf<BF16IN>(prs, lo, ro);
             zv[k][1] = load_raw_buf<BF16IN>(prs, lo + 64 * kElt, ro);
         }
@@ -1970,11 +2022,11 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
 #pragma unroll
         for (int k = 0; k < kPairs; k++) asm volatile("" ::"v"(zv[k][0]), "v"(zv[k][1]));
     };
-    // conv1d + SiLU of block bb into its rows (zero rows past the end); log
-    // decay and beta (0 and 0 past the end) of its tokens
-    auto conv_pass = [&](int bb) {
-        const int nb = min(kDnChunk, a.n_tok - bb * kDnChunk);
-        float(*x)[4 * 128 + 4] = xs[bb % 3];
+    // conv1d + SiLU of stream position q into its rows (zero rows past the
+    // end); log decay and beta (0 and 0 past the end) of its tokens
+    auto conv_pass = [&](int q) {
+        const int nb = min(kDnChunk, a.n_tok - (q % nblk) * kDnChunk);
+        float(*x)[4 * 128 + 4] = xs[q % 3];
 #pragma unroll
         for (int i = 0; i < kDnChunk; i++) {
             if (i < nb) {
@@ -1999,22 +2051,22 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 l_a = sp * a_g;
                 be = sigmoid_f(raw_f<BF16IN>(braw_n));
             }
-            lg[bb % 3][u & 1][ab_t] = l_a;
-            bt[bb % 3][u & 1][ab_t] = be;
+            lg[q % 3][ab_h][ab_t] = l_a;
+            bt[q % 3][ab_h][ab_t] = be;
         }
     };
-    // q/k normalisation in place (helpers 4..7) of block bb
-    auto norm_pass = [&](int bb) {
-        const int nb = min(kDnChunk, a.n_tok - bb * kDnChunk);
+    // q/k normalisation in place (helpers 4..7) of stream position q
+    auto norm_pass = [&](int q) {
+        const int nb = min(kDnChunk, a.n_tok - (q % nblk) * kDnChunk);
         if (hw >= 4 && g16 < nb) {
-            float(*x)[4 * 128 + 4] = xs[bb % 3];
-            float q[kDnCols], k[kDnCols];
-            dn_qk(x[g16], col0, a.eps, q, k);
+            float(*x)[4 * 128 + 4] = xs[q % 3];
+            float qv[kDnCols], kv[kDnCols];
+            dn_qk(x[g16], col0, a.eps, qv, kv);
 #pragma unroll
             for (int j = 0; j < kDnCols; j += 4) {
                 const int cc = col0 + (j ? kSsmDk / 2 : 0);
-                *reinterpret_cast<float4*>(&x[g16][cc]) = make_float4(q[j], q[j + 1], q[j + 2], q[j + 3]);
-                *reinterpret_cast<float4*>(&x[g16][128 + cc]) = make_float4(k[j], k[j + 1], k[j + 2], k[j + 3]);
+                *reinterpret_cast<float4*>(&x[g16][cc]) = make_float4(qv[j], qv[j + 1], qv[j + 2], qv[j + 3]);
+                *reinterpret_cast<float4*>(&x[g16][128 + cc]) = make_float4(kv[j], kv[j + 1], kv[j + 2], kv[j + 3]);
             }
         }
     };
@@ -2049,21 +2101,23 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             for (int i = 0; i < kDnChunk; i++) fc[cur][lane][i] = dn_exp(run - lg[cur][lane][i]);
         }
     };
-    // gated RMSNorm of block bb's (token, v-head) pairs, 128 dims per wave;
-    // pairs past the end or of a block before the first are computed on
-    // stale data and their stores discarded
-    auto out_pass = [&](int bb) {
-        const int nb = min(kDnChunk, a.n_tok - bb * kDnChunk);
-        const int tok0 = bb * kDnChunk;
+    // gated RMSNorm of stream position q's (token, v-head) pairs, 128 dims
+    // per wave; pairs past the end or of a position before the first are
+    // computed on stale data and their stores discarded
+    auto out_pass = [&](int q) {
+        const int item = item_at(q), seq = item / kSsmKHeads, kh = item % kSsmKHeads;
+        const int tok0 = (max(q, 0) % nblk) * kDnChunk;
+        const int nb = min(kDnChunk, a.n_tok - tok0);
+        const __amdgpu_buffer_rsrc_t ors = out_rs(seq);
 #pragma unroll
         for (int k = 0; k < kPairs; k++) {
             const int p = hw + k * kDnHelpWaves;
             const int pt = p >> 1, pvl = p & 1, pvh = kh + kSsmKHeads * pvl;
-            const float* o_row = os[bb & 1][pt][pvl];
+            const float* o_row = os[q & 1][pt][pvl];
             const float o0 = o_row[lane], o1 = o_row[lane + 64];
             const float ss = wave_sum(fmaf(o0, o0, o1 * o1));
             const float rms = dn_rsqrt(ss / kSsmDv + a.eps);
-            const bool ok = bb >= 0 && p < 2 * nb;  // uniform
+            const bool ok = q >= 0 && p < 2 * nb;  // uniform
             const uint32_t ob = ((uint32_t)(tok0 + pt) * (kSsmVHeads * kSsmDv) + (uint32_t)pvh * kSsmDv) * osz;
 #pragma unroll
             for (int h2 = 0; h2 < 2; h2++) {
@@ -2083,10 +2137,10 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
     request_x(0);
     out_pass(-4);
     request_z(-3);
-    for (int bb = -2; bb < nblk; bb++) {
+    for (int bb = -2; bb < n_pos; bb++) {
         const int cur = bb < 0 ? 0 : bb % 3;
-        // Phase A: L, T (helpers 0, 1) and M (helpers 2, 3) of block bb; norms
-        // of block bb + 1
+        // Phase A: L, T (helpers 0, 1) and M (helpers 2, 3) of position bb;
+        // norms of position bb + 1
         if (bb >= 0) {
             if (hw < 2) {
                 // L for v-head hw: strict lower, beta_t e^{g_t - g_s} k_t.k_s
@@ -2134,13 +2188,21 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 }
             }
         }
-        if (bb + 1 >= 0 && bb + 1 < nblk) norm_pass(bb + 1);
+        if (bb + 1 >= 0 && bb + 1 < n_pos) norm_pass(bb + 1);
         lds_barrier();
-        // Phase B: K K^T, Q K^T, prefix sums of block bb + 1; conv and gates
-        // of block bb + 2; output norm of block bb - 1
-        if (bb + 1 >= 0 && bb + 1 < nblk) gram_pass(bb + 1);
+        // Phase B: K K^T, Q K^T, prefix sums of position bb + 1; conv and
+        // gates of position bb + 2 (switching items at a boundary); output
+        // norm of position bb - 1
+        if (bb + 1 >= 0 && bb + 1 < n_pos) gram_pass(bb + 1);
         use_x();
-        if (bb + 2 < nblk) conv_pass(bb + 2);
+        if (bb + 2 < n_pos) {
+            if ((bb + 2) % nblk == 0) {
+                if (cv_item >= 0) conv_done();
+                cv_item = item_at(bb + 2);
+                conv_item(cv_item);
+            }
+            conv_pass(bb + 2);
+        }
         request_x(bb + 3);
         use_z();
         out_pass(bb - 1);
@@ -2148,10 +2210,8 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
         lds_barrier();
     }
     use_z();
-    out_pass(nblk - 1);
-    conv[ch] = w0;
-    conv[kSsmC + ch] = w1;
-    conv[2 * kSsmC + ch] = w2;
+    out_pass(n_pos - 1);
+    conv_done();
 }
 
 constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel
@@ -2420,15 +2480,23 @@ int launch_deltanet(const DeltaNetArgs& a, void* stream) {
         else
             hipLaunchKernelGGL(deltanet_decode_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
     } else if (a.n_tok >= kDnChunk) {
-        const dim3 mblock(kDnMfmaThreads);
+        // persistent: at most one workgroup per CU (its LDS needs a CU)
+        static int n_cu = 0;
+        if (!n_cu) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+                n_cu = 256;
+        }
+        const dim3 mgrid(std::min(a.n_seqs * kSsmKHeads, n_cu)), mblock(kDnMfmaThreads);
         if (a.in_bf16 && a.out_bf16)
-            hipLaunchKernelGGL((deltanet_mfma_kernel<true, true>), grid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<true, true>), mgrid, mblock, 0, (hipStream_t)stream, a);
         else if (a.in_bf16)
-            hipLaunchKernelGGL((deltanet_mfma_kernel<true, false>), grid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<true, false>), mgrid, mblock, 0, (hipStream_t)stream, a);
         else if (a.out_bf16)
-            hipLaunchKernelGGL((deltanet_mfma_kernel<false, true>), grid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<false, true>), mgrid, mblock, 0, (hipStream_t)stream, a);
         else
-            hipLaunchKernelGGL((deltanet_mfma_kernel<false, false>), grid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<false, false>), mgrid, mblock, 0, (hipStream_t)stream, a);
     } else if (a.in_bf16) {
         hipLaunchKernelGGL(deltanet_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
     } else {
