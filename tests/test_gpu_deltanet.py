@@ -58,7 +58,7 @@ def run_case(in_dtype, out_dtype, n_tok, n_seqs, seed, layer=1):
     h = kvc.hip()
     rng = np.random.default_rng(seed)
     conv_w, dtb, a, nw = weights(seed + 1)
-    with ctx_ssm() as ctx:
+    with ctx_ssm(max_seqs=max(4, n_seqs)) as ctx:
         seqs = [ctx.seq_create() for _ in range(n_seqs)]
         S0, C0 = [], []
         for s in seqs:
@@ -251,6 +251,16 @@ def test_deltanet_matrix_form_chunks_match_oracle(n_tok):
     token-by-token kernels."""
     say(f"deltanet matrix form, {n_tok} tokens")
     run_case(kvc.DTYPE_BF16, kvc.DTYPE_F32, n_tok=n_tok, n_seqs=2, seed=7700 + n_tok)
+
+
+def test_deltanet_matrix_form_items_span_workgroups():
+    """The matrix-form kernel is persistent: with more (session, k-head)
+    items than CUs a workgroup runs several items as one stream of blocks,
+    switching state slices and conv windows between them.  20 sessions = 320
+    items on a 256-CU device, 24 tokens each (a full and a partial block per
+    item), every session against the oracle."""
+    say("deltanet matrix form, 20 sessions x 24 tokens (items span workgroups)")
+    run_case(kvc.DTYPE_BF16, kvc.DTYPE_F32, n_tok=24, n_seqs=20, seed=7700, layer=1)
 
 
 def test_deltanet_matrix_form_bf16_out():
