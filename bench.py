@@ -297,6 +297,23 @@ def cpu_baseline_c(P, n_q=128):
 
     O = _oracle()
     cores = host_cores()
+    # append: the oracle's cache append (src/engine.cpp:2885-2889) of 8
+    # sessions' 128-token chunks into host caches, one thread
+    n_app = 8
+    k_new = O.normal_bf16(n_q * ROW, SEED + 300)
+    v_new = O.normal_bf16(n_q * ROW, SEED + 301)
+    caches = [(np.empty((int(p_) + n_q) * ROW, np.uint16), np.empty((int(p_) + n_q) * ROW, np.uint16))
+              for p_ in P[:n_app]]
+    for kc_, vc_ in caches:
+        kc_.fill(0)
+        vc_.fill(0)
+    t0 = time.perf_counter()
+    for (kc_, vc_), p_ in zip(caches, P[:n_app]):
+        O.L().orc_cache_append(kc_.ctypes.data, vc_.ctypes.data, NKV, D, int(p_), n_q, k_new.ctypes.data,
+                               v_new.ctypes.data)
+    a_s = time.perf_counter() - t0
+    a_bytes = n_app * n_q * 2 * 2 * ROW * 2  # K and V rows, read + write
+    del caches
     # gather: reference-layout copies of 8 sessions' reused K and V
     srcs = [np.ones(int(p_) * ROW, np.uint16) for p_ in P[:8]]
     dsts = [np.empty_like(x_) for x_ in srcs]
@@ -328,11 +345,12 @@ def cpu_baseline_c(P, n_q=128):
     q_s = time.perf_counter() - t0
     q_bytes = 256 * ((NQ * 2 * D + 2 * ROW) * 2 + 2 * NQ * D * 2 + 2 * ROW * 2)
     return {"kind": "port", "cores": cores,
+            "append_GBps_1thread": round(a_bytes / a_s / 1e9, 2),
             "gather_GBps": round(g_bytes / g_s / 1e9, 2),
             "prefill_TFLOPs": round(p_flops / p_s / 1e12, 4),
             "prefill_us_per_layer": round(all_flops / (p_flops / p_s) * 1e6, 1),
             "qkv_append_GBps_1thread": round(q_bytes / q_s / 1e9, 3),
-            "sample": f"gather of 8 sessions (1 thread); oracle causal prefill of {len(samp)} sessions, one per "
+            "sample": f"append of 8 sessions' 128-token chunks (1 thread); gather of 8 sessions (1 thread); oracle causal prefill of {len(samp)} sessions, one per "
                       f"thread, scaled to the 64 sessions' flops; producer of 256 tokens (1 thread) "
                       f"({cpu_model()})"}
 
