@@ -4,6 +4,7 @@
 //
 // All K/V traffic is bf16; arithmetic is fp32 (v_dot2_f32_bf16 for q.k).
 // Softmax runs in the log2 domain: s2 = (q.k) * scale * log2(e), p = 2^(s2-m).
+#include <atomic>
 #include "kvc_device.h"
 #include "kvc_internal.h"
 
@@ -2480,13 +2481,17 @@ int launch_deltanet(const DeltaNetArgs& a, void* stream) {
         else
             hipLaunchKernelGGL(deltanet_decode_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
     } else if (a.n_tok >= kDnChunk) {
-        // persistent: at most one workgroup per CU (its LDS needs a CU)
-        static int n_cu = 0;
-        if (!n_cu) {
-            int dev = 0;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-                n_cu = 256;
+        // persistent: at most one workgroup per CU (its LDS needs a CU); the
+        // CU count of the current device is looked up once per process
+        static std::atomic<int> cu_count{0};
+        int n_cu = cu_count.load(std::memory_order_relaxed);
+        if (n_cu <= 0) {
+            int dev = 0, v = 0;
+            n_cu = (hipGetDevice(&dev) == hipSuccess &&
+                    hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+                       ? v
+                       : 256;
+            cu_count.store(n_cu, std::memory_order_relaxed);
         }
         const dim3 mgrid(std::min(a.n_seqs * kSsmKHeads, n_cu)), mblock(kDnMfmaThreads);
         if (a.in_bf16 && a.out_bf16)
