@@ -83,6 +83,12 @@ struct Seq {
     std::vector<int32_t> blocks;   // block id per 32-token block
     std::vector<int32_t> tokens;   // committed token ids (when known)
     std::vector<int32_t> entries;  // prefix-index entry per full block, -1 = none
+    // Block pinned on behalf of entries[i] when that entry indexes another
+    // sequence's copy of the same tokens (two sequences filled the block
+    // independently); -1 when the entry indexes this sequence's own block,
+    // which the sequence already holds.  The pin keeps the entry live, so
+    // entries[i] stays a valid parent for block i + 1.
+    std::vector<int32_t> pins;
     bool state_dirty = false;      // recurrent state must be zeroed before its next use
 };
 
@@ -224,16 +230,35 @@ int32_t find_entry(kvc_ctx* c, uint64_t h, int32_t parent, const int32_t* tok) {
     return it->second;
 }
 
+// Keep the first k index entries of s, dropping the pins of the rest.
+void drop_entries(kvc_ctx* c, Seq& s, size_t k) {
+    while (s.entries.size() > k) {
+        if (s.pins.back() >= 0) unref_block(c, s.pins.back());
+        s.entries.pop_back();
+        s.pins.pop_back();
+    }
+}
+
+void push_entry(kvc_ctx* c, Seq& s, int32_t e, int32_t own_block) {
+    int32_t pin = -1;
+    if (e >= 0 && c->entries[e].block != own_block) {
+        pin = c->entries[e].block;
+        c->refcnt[pin]++;
+    }
+    s.entries.push_back(e);
+    s.pins.push_back(pin);
+}
+
 // Register the full blocks of s that have no entry yet.
 void register_blocks(kvc_ctx* c, Seq& s) {
     const int bt = c->cfg.block_tokens;
     const bool weak = c->cfg.flags & KVC_FLAG_WEAK_HASH;
     const int full = s.len / bt;
-    if ((int)s.entries.size() > full) s.entries.resize(full);
+    drop_entries(c, s, (size_t)full);
     for (int i = (int)s.entries.size(); i < full; i++) {
         const int32_t parent = i == 0 ? -1 : s.entries[i - 1];
         if (i > 0 && parent < 0) {  // chain broken earlier (collision)
-            s.entries.push_back(-1);
+            push_entry(c, s, -1, -1);
             continue;
         }
         const uint64_t ph = i == 0 ? kHashRoot : c->entries[parent].hash;
@@ -243,7 +268,7 @@ void register_blocks(kvc_ctx* c, Seq& s) {
         if (it != c->index.end()) {
             const int32_t e = find_entry(c, h, parent, tok);
             if (e >= 0) touch_entry(c, e);
-            s.entries.push_back(e);  // -1 on a collision: not registered
+            push_entry(c, s, e, s.blocks[i]);  // -1 on a collision: not registered
             continue;
         }
         const int32_t e = new_entry(c);
@@ -262,7 +287,7 @@ void register_blocks(kvc_ctx* c, Seq& s) {
             if (p.n_children++ == 0) leaf_erase(c, parent);
         }
         leaf_insert(c, e);
-        s.entries.push_back(e);
+        push_entry(c, s, e, s.blocks[i]);
     }
 }
 
@@ -715,7 +740,7 @@ int kvc_seq_reset(kvc_ctx* c, int32_t seq) {
     Seq& s = c->seqs[seq];
     s.len = s.pending = 0;
     s.tokens.clear();
-    s.entries.clear();
+    drop_entries(c, s, 0);
     s.tokens_known = true;
     s.state_dirty = c->cfg.n_ssm_layers > 0;
     return KVC_OK;
@@ -741,9 +766,19 @@ int kvc_seq_truncate(kvc_ctx* c, int32_t seq, int32_t len) {
     if (s.pending) return set_err(KVC_ERR_STATE, "sequence %d has %d uncommitted tokens", seq, s.pending);
     if (len < 0 || len > s.len) return set_err(KVC_ERR_RANGE, "truncate to %d outside [0, %d]", len, s.len);
     release_tail(c, seq, (len + kBlockTok - 1) / kBlockTok);
+    drop_entries(c, s, (size_t)(len / kBlockTok));
+    if (c->cfg.n_ssm_layers > 0 && len < s.len) {
+        // The recurrent state cannot be rolled back: it still holds the
+        // dropped tokens.  K/V and state committed from here on are no longer
+        // a function of the token ids, so they must not be keyed by them:
+        // the sequence stops feeding the prefix index and the boundary
+        // snapshots until a reset or a snapshot restore.  The blocks it
+        // indexed before the truncation stay valid.
+        s.tokens_known = false;
+        s.tokens.clear();
+    }
     s.len = len;
     if (s.tokens_known) s.tokens.resize(len);
-    if ((int32_t)s.entries.size() > len / kBlockTok) s.entries.resize(len / kBlockTok);
     return KVC_OK;
 }
 
@@ -791,7 +826,7 @@ int kvc_seq_reserve(kvc_ctx* c, const int32_t* seqs, int32_t n_seqs, int32_t n_t
             c->cow_copies.push_back({g.cow_src, g.block});
             unref_block(c, g.cow_src);
             s.blocks[g.idx] = g.block;
-            if ((int32_t)s.entries.size() > g.idx) s.entries.resize(g.idx);
+            drop_entries(c, s, (size_t)g.idx);
         } else {
             s.blocks.push_back(g.block);
         }
@@ -939,8 +974,11 @@ int kvc_prefix_match(kvc_ctx* c, int32_t seq, const int32_t* tokens, int32_t n, 
     s.len = reuse_blocks * bt;
     s.tokens.assign(tokens, tokens + s.len);
     s.tokens_known = true;
-    s.entries.assign(res.begin(), res.begin() + mapped);
-    for (int i = 0; i < mapped; i++) touch_entry(c, res[i]);
+    drop_entries(c, s, 0);
+    for (int i = 0; i < mapped; i++) {
+        push_entry(c, s, res[i], s.blocks[i]);  // its own block: no pin
+        touch_entry(c, res[i]);
+    }
     int rc = flush_table(c, stream);
     if (rc) return rc;
     if (!rs_seq.empty() && (rc = launch_snapshots(c, rs_seq, rs_snap, rs_first, true, false, true, stream))) return rc;
@@ -1288,13 +1326,15 @@ int kvc_snapshot_save(kvc_ctx* c, const int32_t* seqs, int32_t n_seqs, int32_t* 
         if (s.len <= 0 || s.len % iv)
             return set_err(KVC_ERR_STATE, "sequence %d length %d is not a positive multiple of %d", seqs[i], s.len, iv);
     }
+    // Count the slots first (free, or held by an unpinned snapshot that may
+    // be evicted), so that a save that cannot fit fails with no side effect.
+    int32_t avail = 0;
+    for (const Snapshot& sn : c->snaps) avail += !sn.live || !sn.pinned;
+    if (avail < n_seqs)
+        return set_err(KVC_ERR_NOMEM, "snapshot pool full: %d slots available, %d needed", avail, n_seqs);
     std::vector<int32_t> ss, sl, fb;
     for (int32_t i = 0; i < n_seqs; i++) {
-        const int32_t id = alloc_snapshot(c);
-        if (id < 0) {
-            for (int32_t j : sl) c->snaps[j] = Snapshot();
-            return set_err(KVC_ERR_NOMEM, "snapshot pool full (%zu slots pinned)", c->snaps.size());
-        }
+        const int32_t id = alloc_snapshot(c);  // cannot fail: counted above
         const Seq& s = c->seqs[seqs[i]];
         Snapshot& sn = c->snaps[id];
         sn.live = true;
@@ -1350,13 +1390,13 @@ int kvc_snapshot_restore(kvc_ctx* c, const int32_t* seqs, const int32_t* snap_id
             set_table(c, seqs[i], keep / kBlockTok + b, nb);
         }
         s.len = sn.boundary;
-        if ((int32_t)s.entries.size() > keep / kBlockTok) s.entries.resize(keep / kBlockTok);
+        drop_entries(c, s, (size_t)(keep / kBlockTok));
         if (same_prefix) {
             s.tokens = sn.tokens;
             s.tokens_known = true;
         } else {
             s.tokens.clear();
-            s.entries.clear();
+            drop_entries(c, s, 0);
             s.tokens_known = false;
         }
         sn.tick = ++c->tick;

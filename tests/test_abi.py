@@ -251,3 +251,95 @@ def test_snapshot_requires_boundary_and_device():
         with pytest.raises(kvc.KvcError) as e:
             c.snapshot_save([a])
         assert e.value.code == kvc.KVC_ERR_NO_DEVICE
+
+
+def test_duplicate_block_entry_is_pinned_against_eviction():
+    # Two sequences fill the same tokens in their own blocks; the second finds
+    # the first's index entry for block 0.  After the first is released the
+    # entry must stay live while the second records it as the parent of its
+    # block 1: evicting it would let another chain's entry take its slot and
+    # the second sequence's block 1 would be indexed under a foreign prefix.
+    rng = np.random.default_rng(11)
+    T = rng.integers(0, 151936, 64).astype(np.int32)
+    U = rng.integers(0, 151936, 128).astype(np.int32)
+    with host_ctx(pool_blocks=6) as c:
+        a, b = c.seq_create(), c.seq_create()
+        for s in (a, b):
+            c.reserve([s], 40)
+            c.commit([s], 40, T[:40])
+        c.seq_release(a)  # A's block 0 stays: indexed, and pinned by B
+        st = c.stats()
+        assert st.free_blocks == 3 and st.indexed_blocks == 1 and st.cached_blocks == 0
+        cc = c.seq_create()
+        with pytest.raises(kvc.KvcError) as e:
+            c.reserve([cc], 128)  # would need to evict the pinned entry
+        assert e.value.code == kvc.KVC_ERR_NOMEM
+        c.reserve([cc], 96)
+        c.commit([cc], 96, U[:96])
+        c.reserve([b], 24)
+        c.commit([b], 24, T[40:64])  # B's block 1 registers under T's block 0
+        d = c.seq_create()
+        x = np.array([5], np.int32)
+        assert c.prefix_match(d, np.concatenate([U[:32], T[32:64], x])) == 32
+        c.seq_release(d)
+        d = c.seq_create()
+        assert c.prefix_match(d, np.concatenate([T, x])) == 64
+        c.seq_release(d)
+        # releasing B drops its pin: the entry is held by the index alone
+        c.seq_release(b)
+        c.seq_release(cc)
+        st = c.stats()
+        assert st.free_blocks + st.cached_blocks == 6
+
+
+def test_pins_dropped_on_truncate_and_reset():
+    rng = np.random.default_rng(12)
+    T = rng.integers(0, 151936, 96).astype(np.int32)
+    with host_ctx(pool_blocks=16) as c:
+        a, b = c.seq_create(), c.seq_create()
+        for s in (a, b):
+            c.reserve([s], 96)
+            c.commit([s], 96, T)
+        c.seq_release(a)
+        assert c.stats().free_blocks == 16 - 6  # B's 3 + A's 3 pinned by B
+        c.seq_truncate(b, 40)  # drops B's entries 1, 2 and their pins
+        assert c.stats().free_blocks == 16 - 2 - 3
+        assert c.stats().cached_blocks == 2
+        c.seq_reset(b)
+        st = c.stats()
+        assert st.free_blocks == 16 - 3 and st.cached_blocks == 3
+
+
+def test_hybrid_truncate_stops_keying_by_tokens():
+    # The recurrent state cannot be rolled back, so after a truncation the
+    # sequence's later blocks and boundary snapshots are not keyed by tokens.
+    rng = np.random.default_rng(13)
+    T = rng.integers(0, 151936, 512).astype(np.int32)
+    with host_ctx(n_ssm_layers=24, snapshot_slots=8) as c:
+        a = c.seq_create()
+        c.reserve([a], 200)
+        c.commit([a], 200, T[:200])
+        c.seq_truncate(a, 100)
+        c.reserve([a], 156)
+        c.commit([a], 156, T[100:256])  # lands on the 256 boundary
+        assert c.stats().snapshots == 0
+        b = c.seq_create()
+        assert c.prefix_match(b, np.concatenate([T[:256], [1]]).astype(np.int32)) == 0
+        c.seq_release(b)
+        # a reset makes the sequence keyed again
+        c.seq_reset(a)
+        c.reserve([a], 256)
+        c.commit([a], 256, T[:256])
+        assert c.stats().snapshots == 1
+        b = c.seq_create()
+        assert c.prefix_match(b, np.concatenate([T[:256], [1]]).astype(np.int32)) == 256
+    # a pure-attention context keeps keying after a truncation
+    with host_ctx() as c:
+        a = c.seq_create()
+        c.reserve([a], 200)
+        c.commit([a], 200, T[:200])
+        c.seq_truncate(a, 100)
+        c.reserve([a], 156)
+        c.commit([a], 156, T[100:256])
+        b = c.seq_create()
+        assert c.prefix_match(b, np.concatenate([T[:256], [1]]).astype(np.int32)) == 256
