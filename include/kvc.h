@@ -77,6 +77,14 @@ enum { KVC_DTYPE_F32 = 0, KVC_DTYPE_BF16 = 1 };
  * each other. */
 #define KVC_FLAG_DECODE_SPLIT_D 0x2u
 #define KVC_FLAG_DECODE_NO_SPLIT_D 0x4u
+/* Transcendentals.  By default the library computes the reference's
+ * Schraudolph (1999) approximations (src/engine.cpp:2349-2376): the output
+ * gate sigma(gate) of decode and prefill attention (:3563, :2923), bit-exact
+ * with fast_sigmoidf for every bf16 gate value, and in the Gated-DeltaNet
+ * step the SiLU of the conv output and of z, the beta sigmoid and the exp in
+ * softplus (:2626, :2671, :2674, :2714).  This flag selects exact functions
+ * instead (hardware exp/log/rcp, within 2 ulp). */
+#define KVC_FLAG_EXACT_MATH 0x8u
 
 typedef struct kvc_config {
     int32_t n_attn_layers;     /* full-attention layers (8, model_config.h:8,34) */

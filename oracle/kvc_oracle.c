@@ -13,8 +13,13 @@
  *   f32_to_bf16_rne      exhaustive: nearest-even by exact comparison in fp64
  *                        over every bf16 neighbourhood; NaN/Inf cases
  *   f32_to_bf16_trunc    bit identity (top 16 bits)
- *   fast_expf            Schraudolph formula constants checked at x = 0,
- *                        ln2 multiples and clamps; error bound 4% vs exp
+ *   fast_expf(_rne)      every finite bf16 input and 20000 random fp32
+ *                        inputs against an exact rational model: the fused
+ *                        multiply-add rounded once to fp32, then truncated
+ *                        (rounded to nearest even); an unfused multiply-add
+ *                        fails it; constants at x = 0, ln2 multiples, clamps
+ *   sigmoid/silu mode 1  every finite bf16 input against the same model with
+ *                        each fp32 step (add, divide, multiply) exactly rounded
  *   cache_append/gather  byte equality + canary (untouched slots unchanged)
  *   decode_attn          fp64 two-pass softmax brute force; L=1 -> v0;
  *                        identical keys -> mean(V); one dominant key -> V_j;
@@ -144,12 +149,31 @@ void orc_bf16_to_f32_n(const uint16_t* src, float* dst, size_t n) {
     for (size_t i = 0; i < n; i++) dst[i] = orc_bf16_to_f32(src[i]);
 }
 
-/* Schraudolph (1999) exp: clamp to [-88, 88], then the IEEE-754 bit trick
- * with slope 2^23/ln2 and bias 127*2^23 (src/engine.cpp:2349-2356). */
+/* Schraudolph (1999) exp as the compiled reference computes it
+ * (src/engine.cpp:2349-2356): clamp to [-88, 88], then the fp32 bit pattern
+ * (int32)(12102203 x + 1065353216), slope 2^23/ln2 and bias 127*2^23.  The
+ * reference is built with -ffast-math for an FMA-capable host (Makefile:47,
+ * -march=native on an EPYC 9254 whose flags list fma,
+ * reference_system_info/lscpu.txt), so clang fuses the multiply-add (probe:
+ * clang -O3 -ffast-math -march=znver4 emits vfmadd213ss + vcvttss2si for this
+ * expression).  The oracle is built with contraction off and writes the
+ * fused operation out.  The scalar int conversion truncates toward zero. */
 float orc_fast_expf(float x) {
     if (x < -88.0f) x = -88.0f;
     if (x > 88.0f) x = 88.0f;
-    int32_t i = (int32_t)(12102203.0f * x + 1065353216.0f);
+    int32_t i = (int32_t)fmaf(12102203.0f, x, 1065353216.0f);
+    float f;
+    memcpy(&f, &i, 4);
+    return f;
+}
+
+/* The AVX-512 SiLU's exp (src/engine.cpp:2367-2373): the same fused
+ * multiply-add of the clamped -x, converted with _mm512_cvtps_epi32, which
+ * rounds to nearest even under the default MXCSR. */
+float orc_fast_expf_rne(float x) {
+    if (x < -88.0f) x = -88.0f;
+    if (x > 88.0f) x = 88.0f;
+    int32_t i = (int32_t)rintf(fmaf(12102203.0f, x, 1065353216.0f));
     float f;
     memcpy(&f, &i, 4);
     return f;
@@ -158,6 +182,13 @@ float orc_fast_expf(float x) {
 float orc_sigmoid(float x, int mode) {
     if (mode == 1) return 1.0f / (1.0f + orc_fast_expf(-x)); /* :2358-2360 */
     return 1.0f / (1.0f + expf(-x));
+}
+
+/* SiLU x * sigmoid(x).  mode 1 is the AVX-512 form used on the conv output
+ * and the z gate (:2366-2376, called at :2626, :2714, :3227, :3321). */
+float orc_silu(float x, int mode) {
+    if (mode == 1) return x * (1.0f / (1.0f + orc_fast_expf_rne(0.0f - x)));
+    return x * orc_sigmoid(x, 0);
 }
 
 /* ---------------------------------------------------------------------- */
@@ -426,8 +457,6 @@ void orc_qkv_produce(const float* qkv, int n_q, int n_kv, int d, int rope_dim,
 
 /* ---------------------------------------------------------------------- */
 /* Gated-DeltaNet layer step                                                */
-
-static float orc_silu(float x, int fast) { return x * orc_sigmoid(x, fast); }
 
 void orc_deltanet_layer_step(float* conv_state, float* ssm_state, const float* proj,
                              const float* conv_w, const float* dt_bias, const float* a,

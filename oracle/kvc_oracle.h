@@ -41,8 +41,10 @@ uint16_t orc_f32_to_bf16_trunc(float x); /* src/engine.cpp:248-252 */
 float orc_bf16_to_f32(uint16_t b);       /* src/engine.cpp:253-258 */
 void orc_f32_to_bf16_rne_n(const float* src, uint16_t* dst, size_t n);
 void orc_bf16_to_f32_n(const uint16_t* src, float* dst, size_t n);
-float orc_fast_expf(float x);            /* src/engine.cpp:2349-2356 */
+float orc_fast_expf(float x);            /* src/engine.cpp:2349-2356 (fused, truncating) */
+float orc_fast_expf_rne(float x);        /* the AVX-512 SiLU's exp, :2367-2373 (fused, RNE) */
 float orc_sigmoid(float x, int mode);    /* mode 0 exact, 1 = :2358-2360 */
+float orc_silu(float x, int mode);       /* mode 0 exact, 1 = :2366-2376 */
 
 /* ---- cache append / gather (byte copies) ------------------------------ */
 /* src/engine.cpp:3521-3525 (decode) and :2885-2889 (prefill, pos = g_pos+ti) */

@@ -68,6 +68,28 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Schraudolph (1999) exp as the reference computes it (src/engine.cpp:2349-2356):
+// clamp to [-88, 88] (min first, then max), then the fp32 bit pattern of
+// (int32)(12102203 x + 1065353216), slope 2^23/ln2 and bias 127 * 2^23.  The
+// reference is built with -ffast-math for an FMA host, so the multiply-add is
+// one fused operation (v_fma_f32 here, correctly rounded like x86 vfmadd).
+// The scalar helper converts by truncation (v_cvt_i32_f32); the AVX-512 SiLU
+// (:2367-2373) converts with cvtps2dq, round to nearest even (v_rndne_f32
+// first).  After the clamp the sum lies in (0, 2^31), so the conversion never
+// saturates.
+__device__ __forceinline__ float schraudolph_exp(float x) {
+    x = fmaxf(-88.0f, fminf(88.0f, x));
+    return __int_as_float((int)__builtin_fmaf(12102203.0f, x, 1065353216.0f));
+}
+__device__ __forceinline__ float schraudolph_exp_rne(float x) {
+    x = fmaxf(-88.0f, fminf(88.0f, x));
+    return __int_as_float((int)__builtin_rintf(__builtin_fmaf(12102203.0f, x, 1065353216.0f)));
+}
+// The reference's gate sigmoid, fast_sigmoidf (src/engine.cpp:2358-2360):
+// 1 / (1 + fast_expf(-x)) with an IEEE division (hipcc rounds fp32 division
+// correctly by default), bit-exact with that formula for every input but NaN.
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + schraudolph_exp(-x)); }
+
 // Raw buffer access with cache-policy bits.  kCpolSC1 marks an access as
 // coherent at agent (device) scope: stores write through the XCD's L2 and
 // loads do not take a stale line from it, so data can pass between

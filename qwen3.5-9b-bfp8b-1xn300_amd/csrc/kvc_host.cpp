@@ -1148,6 +1148,7 @@ int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
         a.chunk_blocks = cb;
         a.total_chunks = (int32_t)total_chunks;
         a.d_parts = d_parts;
+        a.gate_ref = !(c->cfg.flags & KVC_FLAG_EXACT_MATH);
         a.n_items = (int32_t)(total_chunks * kKvHeads * d_parts);
         a.per_xcd = (a.n_items + 7) / 8;
         int e = launch_decode(a, stream);
@@ -1188,6 +1189,7 @@ int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_s
         a.table_stride = c->max_blocks;
         a.n_seqs = n;
         a.n_q = n_q;
+        a.gate_ref = !(c->cfg.flags & KVC_FLAG_EXACT_MATH);
         a.n_groups = n * kKvHeads;
         for (int32_t j = 0; j < n; j++) a.seq_order[j] = j;
         std::stable_sort(a.seq_order, a.seq_order + n,
@@ -1307,6 +1309,7 @@ int kvc_deltanet_step(kvc_ctx* c, int32_t ssm_layer, const int32_t* seqs, int32_
         d.out_bf16 = out_dtype == KVC_DTYPE_BF16;
         d.n_seqs = n;
         d.n_tok = n_tok;
+        d.ref_math = !(k.flags & KVC_FLAG_EXACT_MATH);
         for (int32_t j = 0; j < n; j++) d.slot[j] = seqs[i0 + j];
         int e = launch_deltanet(d, stream);
         if (e) return hip_err((hipError_t)e, "deltanet launch");

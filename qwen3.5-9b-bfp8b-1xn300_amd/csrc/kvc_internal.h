@@ -72,6 +72,8 @@ struct DecodeArgs {
     int32_t n_items;        // total_chunks * Hkv * d_parts
     int32_t per_xcd;        // ceil(n_items / 8)
     int32_t d_parts;        // output-dim parts per (chunk, head): 1 or 2
+    int32_t gate_ref;       // 1: the reference's Schraudolph gate sigmoid; 0: exact
+    int32_t pad;
     int32_t slot[kMaxBatch];
     int32_t kv_len[kMaxBatch];       // keys attended (new token included)
     int32_t chunk_begin[kMaxBatch + 1];
@@ -142,6 +144,8 @@ struct DeltaNetArgs {
     int32_t out_bf16;
     int32_t n_seqs;
     int32_t n_tok;
+    int32_t ref_math;       // 1: the reference's Schraudolph SiLU / sigmoid / softplus
+    int32_t pad;
     int32_t slot[kMaxBatch];
 };
 
@@ -182,7 +186,7 @@ struct PrefillArgs {
     int32_t table_stride;
     int32_t n_seqs;
     int32_t n_q;
-    int32_t pad;
+    int32_t gate_ref;           // 1: the reference's Schraudolph gate sigmoid; 0: exact
     int32_t n_groups;           // n_seqs * Hkv (sequence, kv head) groups
     int32_t pad2;
     int32_t slot[kMaxBatch];

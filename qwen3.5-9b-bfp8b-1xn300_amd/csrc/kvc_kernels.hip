@@ -316,23 +316,28 @@ __device__ __forceinline__ void merge_waves(const WaveState& st, DecodeSmem& sm,
     }
 }
 
-// sigmoid to within a few ulp: v_exp_f32 and v_rcp_f32 (the reference uses
-// a Schraudolph approximation with ~4% exp error, src/engine.cpp:2349-2360)
+// sigmoid to within a few ulp: v_exp_f32 and v_rcp_f32 (KVC_FLAG_EXACT_MATH)
 __device__ __forceinline__ float sigmoidf_exact(float x) {
     return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-x * 1.4426950408889634f));
+}
+// The output gate sigma(gate) (src/engine.cpp:3563 decode, :2923 prefill):
+// the reference's Schraudolph sigmoid by default, the exact one on request.
+// ref is a kernel argument, uniform over the launch.
+__device__ __forceinline__ float gate_sigmoid(float x, int ref) {
+    return ref ? sigmoid_ref(x) : sigmoidf_exact(x);
 }
 
 // out row = A / L (* sigmoid(gate)), written as bf16 (RNE) or fp32.
 __device__ __forceinline__ void write_out(void* out, int out_bf16, size_t row_off, int d0,
-                                          const uint16_t* gate_row, float L, const float (&A)[4]) {
+                                          const uint16_t* gate_row, int gate_ref, float L, const float (&A)[4]) {
     const float inv = __builtin_amdgcn_rcpf(L);
     float o[4] = {A[0] * inv, A[1] * inv, A[2] * inv, A[3] * inv};
     if (gate_row) {
         const uint2 gw = *reinterpret_cast<const uint2*>(gate_row + d0);
-        o[0] *= sigmoidf_exact(bf16lo(gw.x));
-        o[1] *= sigmoidf_exact(bf16hi(gw.x));
-        o[2] *= sigmoidf_exact(bf16lo(gw.y));
-        o[3] *= sigmoidf_exact(bf16hi(gw.y));
+        o[0] *= gate_sigmoid(bf16lo(gw.x), gate_ref);
+        o[1] *= gate_sigmoid(bf16hi(gw.x), gate_ref);
+        o[2] *= gate_sigmoid(bf16lo(gw.y), gate_ref);
+        o[3] *= gate_sigmoid(bf16hi(gw.y), gate_ref);
     }
     if (out_bf16) {
         uint2 w;
@@ -626,7 +631,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     const size_t orow = ((size_t)s * kQHeads + h * kGroup + g) * kHeadDim;
     const uint16_t* grow = a.gate ? a.gate + orow : nullptr;
     if (n_chunks == 1) {
-        if (act) write_out(a.out, a.out_bf16, orow, d0, grow, Lsum, A);
+        if (act) write_out(a.out, a.out_bf16, orow, d0, grow, a.gate_ref, Lsum, A);
         return;
     }
     // publish (m, l, acc) with agent-coherent 16-B stores; once they have all
@@ -715,7 +720,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; j++) Ac[j] = sum_xor32(Ac[j]);
     }
-    if (act) write_out(a.out, a.out_bf16, orow, d0, grow, Lc, Ac);
+    if (act) write_out(a.out, a.out_bf16, orow, d0, grow, a.gate_ref, Lc, Ac);
     if (t == 0) *ctr = 0;
 }
 
@@ -1134,10 +1139,10 @@ void prefill_mfma_kernel(PrefillArgs a) {
             float v4[4] = {o[dt][nt][0] * inv, o[dt][nt][1] * inv, o[dt][nt][2] * inv, o[dt][nt][3] * inv};
             if (a.gate) {
                 const uint2 gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
-                v4[0] *= sigmoidf_exact(bf16lo(gw.x));
-                v4[1] *= sigmoidf_exact(bf16hi(gw.x));
-                v4[2] *= sigmoidf_exact(bf16lo(gw.y));
-                v4[3] *= sigmoidf_exact(bf16hi(gw.y));
+                v4[0] *= gate_sigmoid(bf16lo(gw.x), a.gate_ref);
+                v4[1] *= gate_sigmoid(bf16hi(gw.x), a.gate_ref);
+                v4[2] *= gate_sigmoid(bf16lo(gw.y), a.gate_ref);
+                v4[3] *= gate_sigmoid(bf16hi(gw.y), a.gate_ref);
             }
             if (a.out_bf16) {
                 uint2 w;
@@ -1439,6 +1444,29 @@ __device__ __forceinline__ float dn_rsqrt(float x) { return __builtin_amdgcn_rsq
 __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + dn_exp(-x)); }
 __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
+// Reference math (REF, the default; KVC_FLAG_EXACT_MATH clears it): the
+// reference's Schraudolph forms.  beta = fast_sigmoidf(beta_raw) (scalar exp,
+// truncating conversion, src/engine.cpp:2674 / :3281); SiLU of the conv
+// output and of z is the AVX-512 form (exp converted to nearest even,
+// :2626, :2714, :3227, :3321); softplus takes log(1 + fast_expf(b)) (:2671,
+// :3278).  The reciprocal is v_rcp_f32 (1 ulp): the reference's fast-math
+// build computes x / (1 + e) with an approximate reciprocal too, so no exact
+// bits exist to match there; the bound is tested against the oracle.
+template <bool REF>
+__device__ __forceinline__ float dn_sigmoid(float x) {
+    if constexpr (REF)
+        return __builtin_amdgcn_rcpf(1.0f + schraudolph_exp(-x));
+    else
+        return sigmoid_f(x);
+}
+template <bool REF>
+__device__ __forceinline__ float dn_silu(float x) {
+    if constexpr (REF)
+        return x * __builtin_amdgcn_rcpf(1.0f + schraudolph_exp_rne(0.0f - x));
+    else
+        return silu_f(x);
+}
+
 // sum over the 16 lanes of a DPP row (every lane gets the sum)
 __device__ __forceinline__ float sum16(float x) {
     x += dpp<kDppXor1>(x);
@@ -1502,16 +1530,19 @@ __device__ __forceinline__ void dn_qk(const float* conv_lds, int col0, float eps
     }
 }
 
+template <bool REF>
 __device__ __forceinline__ void dn_gates(float alpha, float braw, float dtb, float av, float& decay, float& beta) {
 #pragma clang fp contract(off)
     const float biased = alpha + dtb;
-    const float sp = biased > 20.0f ? biased : dn_log(1.0f + dn_exp(biased));
+    const float ex = REF ? schraudolph_exp(biased) : dn_exp(biased);
+    const float sp = biased > 20.0f ? biased : dn_log(1.0f + ex);
     decay = dn_exp(sp * av);
-    beta = sigmoid_f(braw);
+    beta = dn_sigmoid<REF>(braw);
 }
 
 // gated RMSNorm of one v-head's 128 outputs (o_row) and the store of dims
 // 32 wi .. +31 (lanes 0..31)
+template <bool REF>
 __device__ __forceinline__ void dn_norm_out(const DeltaNetArgs& a, const float* o_row, int lane, int wi, int vh,
                                             size_t out_row, float z) {
 #pragma clang fp contract(off)
@@ -1520,7 +1551,7 @@ __device__ __forceinline__ void dn_norm_out(const DeltaNetArgs& a, const float* 
     const float rms = dn_rsqrt(ss / kSsmDv + a.eps);
     if (lane < 32) {
         const int d = wi * 32 + lane;
-        const float y = o_row[d] * rms * a.norm_w[d] * silu_f(z);
+        const float y = o_row[d] * rms * a.norm_w[d] * dn_silu<REF>(z);
         const size_t oi = out_row + (size_t)vh * kSsmDv + d;
         if (a.out_bf16)
             static_cast<uint16_t*>(a.out)[oi] = (uint16_t)f32_to_bf16_rne(y);
@@ -1551,7 +1582,7 @@ __device__ __forceinline__ void nt_st4(float* p, float x, float y, float z, floa
     __builtin_nontemporal_store(f32x4{x, y, z, w}, reinterpret_cast<f32x4*>(p));
 }
 
-template <bool BF16IN>
+template <bool BF16IN, bool REF>
 __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void deltanet_kernel(DeltaNetArgs a) {
 #pragma clang fp contract(off)
@@ -1619,7 +1650,7 @@ void deltanet_kernel(DeltaNetArgs a) {
                 sum = fmaf(w1, cw.y, sum);
                 sum = fmaf(w2, cw.z, sum);
                 sum = fmaf(x, cw.w, sum);
-                xs[i][t] = silu_f(sum);
+                xs[i][t] = dn_silu<REF>(sum);
                 w0 = w1;
                 w1 = w2;
                 w2 = x;
@@ -1641,7 +1672,7 @@ void deltanet_kernel(DeltaNetArgs a) {
             const int gt = t >> 1, gvh = kh + kSsmKHeads * (t & 1);
             const size_t row = prow0 + (size_t)(tok0 + gt) * kSsmProj;
             float decay, beta;
-            dn_gates(load_f<BF16IN>(a.proj, row + kAlpha + gvh), load_f<BF16IN>(a.proj, row + kBeta + gvh),
+            dn_gates<REF>(load_f<BF16IN>(a.proj, row + kAlpha + gvh), load_f<BF16IN>(a.proj, row + kBeta + gvh),
                      a.dt_bias[gvh], a.a[gvh], decay, beta);
             gs[gt][t & 1] = make_float2(decay, beta);
         }
@@ -1684,7 +1715,7 @@ void deltanet_kernel(DeltaNetArgs a) {
             for (int h2 = 0; h2 < 2; h2++) {
                 const int d = lane + 64 * h2;
                 const float z = load_f<BF16IN>(a.proj, row + kZ + (size_t)pvh * kSsmDv + d);
-                const float y = o_row[d] * rms * a.norm_w[d] * silu_f(z);
+                const float y = o_row[d] * rms * a.norm_w[d] * dn_silu<REF>(z);
                 if (a.out_bf16)
                     static_cast<uint16_t*>(a.out)[out_row + d] = (uint16_t)f32_to_bf16_rne(y);
                 else
@@ -1775,7 +1806,7 @@ constexpr int kDnMathWaves = 8;
 constexpr int kDnHelpWaves = 8;
 constexpr int kDnMfmaThreads = 64 * (kDnMathWaves + kDnHelpWaves);
 
-template <bool BF16IN, bool BF16OUT>
+template <bool BF16IN, bool BF16OUT, bool REF>
 __global__ __launch_bounds__(kDnMfmaThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void deltanet_mfma_kernel(DeltaNetArgs a) {
 #pragma clang fp contract(off)
@@ -2036,7 +2067,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 sum = fmaf(w1, cw.y, sum);
                 sum = fmaf(w2, cw.z, sum);
                 sum = fmaf(xv, cw.w, sum);
-                x[i][u] = silu_f(sum);
+                x[i][u] = dn_silu<REF>(sum);
                 w0 = w1;
                 w1 = w2;
                 w2 = xv;
@@ -2048,9 +2079,10 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             float l_a = 0.f, be = 0.f;
             if (ab_t < nb) {
                 const float biased = raw_f<BF16IN>(alpha_n) + dtb_g;
-                const float sp = biased > 20.0f ? biased : dn_log(1.0f + dn_exp(biased));
+                const float ex = REF ? schraudolph_exp(biased) : dn_exp(biased);
+                const float sp = biased > 20.0f ? biased : dn_log(1.0f + ex);
                 l_a = sp * a_g;
-                be = sigmoid_f(raw_f<BF16IN>(braw_n));
+                be = dn_sigmoid<REF>(raw_f<BF16IN>(braw_n));
             }
             lg[q % 3][ab_h][ab_t] = l_a;
             bt[q % 3][ab_h][ab_t] = be;
@@ -2123,7 +2155,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
 #pragma unroll
             for (int h2 = 0; h2 < 2; h2++) {
                 const int d = lane + 64 * h2;
-                const float y = o_row[d] * rms * (h2 ? nw1 : nw0) * silu_f(raw_f<BF16IN>(zv[k][h2]));
+                const float y = o_row[d] * rms * (h2 ? nw1 : nw0) * dn_silu<REF>(raw_f<BF16IN>(zv[k][h2]));
                 const uint32_t off = ok ? ob + (uint32_t)d * osz : kDrop;
                 if constexpr (BF16OUT)
                     __builtin_amdgcn_raw_buffer_store_b16((unsigned short)f32_to_bf16_rne(y), ors, off, 0, 0);
@@ -2217,7 +2249,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
 
 constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel
 
-template <bool BF16IN>
+template <bool BF16IN, bool REF>
 __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArgs a) {
 #pragma clang fp contract(off)
     __shared__ float conv_lds[4 * 128];
@@ -2256,7 +2288,7 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArg
     sum = fmaf(c1, a.conv_w[kSsmC + ch], sum);
     sum = fmaf(c2, a.conv_w[2 * kSsmC + ch], sum);
     sum = fmaf(x, a.conv_w[3 * kSsmC + ch], sum);
-    conv_lds[t] = silu_f(sum);
+    conv_lds[t] = dn_silu<REF>(sum);
     conv[ch] = c1;
     conv[kSsmC + ch] = c2;
     conv[2 * kSsmC + ch] = x;
@@ -2264,7 +2296,7 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArg
 
     float q[kDnCols], k[kDnCols], decay, beta;
     dn_qk(conv_lds, col0, a.eps, q, k);
-    dn_gates(alpha, braw, a.dt_bias[vh], a.a[vh], decay, beta);
+    dn_gates<REF>(alpha, braw, a.dt_bias[vh], a.a[vh], decay, beta);
 #pragma unroll
     for (int r = 0; r < kDnRows; r++) {
         float st[kDnCols] = {buf[r % kDnPf][0].x, buf[r % kDnPf][0].y, buf[r % kDnPf][0].z, buf[r % kDnPf][0].w,
@@ -2280,7 +2312,7 @@ __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArg
         nt_st4(dst + kSsmDk / 2, st[4], st[5], st[6], st[7]);
     }
     __syncthreads();
-    dn_norm_out(a, o_lds[vl], lane, wi, vh, (size_t)s * (kSsmVHeads * kSsmDv), z);
+    dn_norm_out<REF>(a, o_lds[vl], lane, wi, vh, (size_t)s * (kSsmVHeads * kSsmDv), z);
 }
 
 // ---------------------------------------------------------------------------
@@ -2471,15 +2503,14 @@ int launch_qkv_append(const QkvArgs& a, void* stream) {
     return (int)hipGetLastError();
 }
 
-int launch_deltanet(const DeltaNetArgs& a, void* stream) {
-    static_assert(kSsmVHeads == 2 * kSsmKHeads && kSsmDk == 128 && kSsmDv == 128,
-                  "one workgroup per k-head and its two v-heads, 4 columns per lane");
+template <bool REF>
+static void launch_deltanet_t(const DeltaNetArgs& a, hipStream_t stream) {
     const dim3 grid(a.n_seqs * kSsmKHeads), block(kDnThreads);
     if (a.n_tok == 1) {
         if (a.in_bf16)
-            hipLaunchKernelGGL(deltanet_decode_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_decode_kernel<true, REF>), grid, block, 0, stream, a);
         else
-            hipLaunchKernelGGL(deltanet_decode_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_decode_kernel<false, REF>), grid, block, 0, stream, a);
     } else if (a.n_tok >= kDnChunk) {
         // persistent: at most one workgroup per CU (its LDS needs a CU); the
         // CU count of the current device is looked up once per process
@@ -2495,18 +2526,27 @@ int launch_deltanet(const DeltaNetArgs& a, void* stream) {
         }
         const dim3 mgrid(std::min(a.n_seqs * kSsmKHeads, n_cu)), mblock(kDnMfmaThreads);
         if (a.in_bf16 && a.out_bf16)
-            hipLaunchKernelGGL((deltanet_mfma_kernel<true, true>), mgrid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<true, true, REF>), mgrid, mblock, 0, stream, a);
         else if (a.in_bf16)
-            hipLaunchKernelGGL((deltanet_mfma_kernel<true, false>), mgrid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<true, false, REF>), mgrid, mblock, 0, stream, a);
         else if (a.out_bf16)
-            hipLaunchKernelGGL((deltanet_mfma_kernel<false, true>), mgrid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<false, true, REF>), mgrid, mblock, 0, stream, a);
         else
-            hipLaunchKernelGGL((deltanet_mfma_kernel<false, false>), mgrid, mblock, 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((deltanet_mfma_kernel<false, false, REF>), mgrid, mblock, 0, stream, a);
     } else if (a.in_bf16) {
-        hipLaunchKernelGGL(deltanet_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
+        hipLaunchKernelGGL((deltanet_kernel<true, REF>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL(deltanet_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
+        hipLaunchKernelGGL((deltanet_kernel<false, REF>), grid, block, 0, stream, a);
     }
+}
+
+int launch_deltanet(const DeltaNetArgs& a, void* stream) {
+    static_assert(kSsmVHeads == 2 * kSsmKHeads && kSsmDk == 128 && kSsmDv == 128,
+                  "one workgroup per k-head and its two v-heads, 4 columns per lane");
+    if (a.ref_math)
+        launch_deltanet_t<true>(a, (hipStream_t)stream);
+    else
+        launch_deltanet_t<false>(a, (hipStream_t)stream);
     return (int)hipGetLastError();
 }
 

@@ -35,6 +35,7 @@ DTYPE_BF16 = 1
 FLAG_WEAK_HASH = 0x1
 FLAG_DECODE_SPLIT_D = 0x2
 FLAG_DECODE_NO_SPLIT_D = 0x4
+FLAG_EXACT_MATH = 0x8  # exact sigmoid / SiLU / softplus instead of the reference's Schraudolph forms
 
 # every symbol include/kvc.h declares
 EXPORTS = [

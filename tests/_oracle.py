@@ -6,6 +6,7 @@ Only tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this.
 from __future__ import annotations
 
 import ctypes
+import math
 import subprocess
 from pathlib import Path
 
@@ -44,7 +45,9 @@ def L() -> ctypes.CDLL:
             "orc_f32_to_bf16_rne_n": (None, [P, P, ctypes.c_size_t]),
             "orc_bf16_to_f32_n": (None, [P, P, ctypes.c_size_t]),
             "orc_fast_expf": (F, [F]),
+            "orc_fast_expf_rne": (F, [F]),
             "orc_sigmoid": (F, [F, I]),
+            "orc_silu": (F, [F, I]),
             "orc_cache_append": (None, [P, P, I, I, I, I, P, P]),
             "orc_cache_gather": (None, [P, P, I, I, I, I, P, P]),
             "orc_decode_attn": (None, [P, P, P, I, I, I, I, F, P, I, P]),
@@ -99,7 +102,7 @@ def normal_bf16(n: int, seed: int, scale: float = 1.0) -> np.ndarray:
 
 # ---- oracle wrappers -------------------------------------------------------
 
-def decode_attn(q, kc, vc, L_, n_q=16, n_kv=4, d=256, scale=1 / 16, gate=None, gate_mode=0):
+def decode_attn(q, kc, vc, L_, n_q=16, n_kv=4, d=256, scale=1 / 16, gate=None, gate_mode=1):
     q = np.ascontiguousarray(q, dtype=np.uint16)
     kc = np.ascontiguousarray(kc, dtype=np.uint16)
     vc = np.ascontiguousarray(vc, dtype=np.uint16)
@@ -109,7 +112,7 @@ def decode_attn(q, kc, vc, L_, n_q=16, n_kv=4, d=256, scale=1 / 16, gate=None, g
     return out
 
 
-def prefill_attn(q, kc, vc, pos0, n, n_q=16, n_kv=4, d=256, scale=1 / 16, gate=None, gate_mode=0):
+def prefill_attn(q, kc, vc, pos0, n, n_q=16, n_kv=4, d=256, scale=1 / 16, gate=None, gate_mode=1):
     q = np.ascontiguousarray(q, dtype=np.uint16)
     kc = np.ascontiguousarray(kc, dtype=np.uint16)
     vc = np.ascontiguousarray(vc, dtype=np.uint16)
@@ -186,7 +189,7 @@ SSM_SCALE = 1.0 / 11.3137                         # :3251
 
 
 def deltanet_layer_step(conv_state, ssm_state, proj, conv_w, dt_bias, a, norm_w, n_v=SSM_NV, n_k=SSM_NK,
-                        dk=SSM_DK, dv=SSM_DV, eps=RMS_EPS, fast=0):
+                        dk=SSM_DK, dv=SSM_DV, eps=RMS_EPS, fast=1):
     """One token through one layer; conv_state / ssm_state (fp32) are updated
     in place; returns the gated-RMSNorm output [n_v * dv]."""
     for arr in (conv_state, ssm_state):
@@ -250,3 +253,71 @@ def assert_attn_close(got, want, atol=2e-2, rel_rms=1e-2, what=""):
     rr = float(np.sqrt((diff ** 2).mean()) / max(np.sqrt((want ** 2).mean()), 1e-30)) if diff.size else 0.0
     assert mx <= atol and rr <= rel_rms, f"{what}: max|diff|={mx:.3e} (atol {atol}), rel rms={rr:.3e} (<= {rel_rms})"
     return mx, rr
+
+
+# ---- exact models of the reference's Schraudolph helpers -------------------
+# Independent of the oracle's code: every fp32 operation is modelled as the
+# exact rational result rounded once to fp32 (nearest even, subnormals and
+# overflow included), so the models pin the oracle bit for bit.
+from fractions import Fraction  # noqa: E402
+
+
+def f32_round(q: Fraction) -> float:
+    """Exact rational -> nearest fp32 (ties to even), as a Python float."""
+    if q == 0:
+        return 0.0
+    sign = -1.0 if q < 0 else 1.0
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if (Fraction(2) ** e) > a:
+        e -= 1
+    e = max(e, -126)  # below the normal range the spacing stays 2^-149
+    ulp = Fraction(2) ** (e - 23)
+    n = a / ulp
+    fl = n.numerator // n.denominator
+    rem = n - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    val = fl * ulp
+    if val >= Fraction(2) ** 128:
+        return sign * math.inf
+    return math.copysign(float(val), sign)
+
+
+def schraudolph_exp_model(x: float, rne: bool) -> float:
+    """src/engine.cpp:2349-2356 (rne = False: scalar, truncating conversion)
+    and the AVX-512 SiLU's exp :2367-2373 (rne = True): clamp, one fused
+    multiply-add rounded to fp32, conversion to int32, bits as fp32."""
+    xc = min(88.0, max(-88.0, x))
+    v = Fraction(f32_round(Fraction(12102203) * Fraction(xc) + 1065353216))
+    if rne:
+        fl = v.numerator // v.denominator
+        rem = v - fl
+        i = fl + (1 if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2) else 0)
+    else:
+        i = int(v)  # toward zero (v > 0 after the clamp)
+    return float(np.array([i], np.int32).view(np.float32)[0])
+
+
+def sigmoid_ref_model(x: float) -> float:
+    """1 / (1 + fast_expf(-x)), src/engine.cpp:2358-2360, each step rounded."""
+    e = schraudolph_exp_model(-x, rne=False)
+    t = f32_round(1 + Fraction(e))
+    return f32_round(Fraction(1) / Fraction(t))
+
+
+def silu_ref_model(x: float) -> float:
+    """x * (1 / (1 + exp_rne(0 - x))), the AVX-512 SiLU :2366-2376."""
+    e = schraudolph_exp_model(0.0 - x, rne=True)
+    t = f32_round(1 + Fraction(e))
+    r = f32_round(Fraction(1) / Fraction(t))
+    if x == 0:
+        return x  # IEEE: (+-0) * r keeps the sign of zero for r > 0
+    return f32_round(Fraction(x) * Fraction(r))
+
+
+def finite_bf16_values() -> np.ndarray:
+    """Every finite bf16 bit pattern (NaN and the infinities excluded) as fp32."""
+    b = np.arange(65536, dtype=np.uint32)
+    f = (b << 16).view(np.float32)
+    return f[np.isfinite(f)]

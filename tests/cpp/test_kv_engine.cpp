@@ -304,7 +304,7 @@ static void test_attention_parity() {
     EXPECT_TRUE(!got.q.empty() && got.q[layer].size() == 16 * 256);
     if (got.q.empty()) return;
     std::vector<float> ref(16 * 256);
-    g_orc_decode(got.q[layer].data(), kc.data(), vc.data(), L, 16, 4, 256, 1.0f / 16.0f, got.gate[layer].data(), 0,
+    g_orc_decode(got.q[layer].data(), kc.data(), vc.data(), L, 16, 4, 256, 1.0f / 16.0f, got.gate[layer].data(), 1,
                  ref.data());
     double maxd = 0, se = 0, sr = 0;
     for (int i = 0; i < 16 * 256; i++) {

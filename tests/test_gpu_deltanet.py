@@ -1,11 +1,15 @@
 """GPU parity of the Gated-DeltaNet layer step (kvc_deltanet_step) against the
-oracle's restatement of src/engine.cpp:3197-3327 with exact exp / sigmoid /
-SiLU (the HIP path's semantics), in place on the library's recurrent and conv
-state.
+oracle's restatement of src/engine.cpp:3197-3327, in place on the library's
+recurrent and conv state.  By default both sides compute the reference's
+Schraudolph SiLU, beta sigmoid and softplus exp (src/engine.cpp:2349-2376,
+oracle fast = 1); contexts with KVC_FLAG_EXACT_MATH are checked against the
+oracle's exact functions (fast = 0).  The two modes differ by ~1e-3 relative
+RMS, a hundred times the bar below, so each check tells them apart.
 
 Bars: the conv window is data movement (bit-exact).  The recurrent state and
 the outputs differ from the oracle only by fp32 summation order (wave tree sums
-vs sequential loops) and by the device's exp/log (within a few ulp of libm):
+vs sequential loops) and by the device's exp/log/reciprocal (within a few ulp of
+libm and IEEE division):
 relative RMS <= 1e-5 and max |diff| <= 1e-4 x max |ref| after every token; bf16
 outputs within half a bf16 ulp plus that fp32 bound of the oracle, and >= 99%
 equal to the oracle rounded to nearest-even.  Running the
@@ -54,11 +58,12 @@ def rel_close(got, want, what):
     assert rms <= 1e-5 and mx <= 1e-4, f"{what}: rel rms {rms:.2e}, max {mx:.2e}"
 
 
-def run_case(in_dtype, out_dtype, n_tok, n_seqs, seed, layer=1):
+def run_case(in_dtype, out_dtype, n_tok, n_seqs, seed, layer=1, exact=False):
     h = kvc.hip()
     rng = np.random.default_rng(seed)
     conv_w, dtb, a, nw = weights(seed + 1)
-    with ctx_ssm(max_seqs=max(4, n_seqs)) as ctx:
+    fast = 0 if exact else 1
+    with ctx_ssm(max_seqs=max(4, n_seqs), flags=kvc.FLAG_EXACT_MATH if exact else 0) as ctx:
         seqs = [ctx.seq_create() for _ in range(n_seqs)]
         S0, C0 = [], []
         for s in seqs:
@@ -94,8 +99,8 @@ def run_case(in_dtype, out_dtype, n_tok, n_seqs, seed, layer=1):
     for i in range(n_seqs):
         cs, S = C0[i].copy(), S0[i].copy()
         for t in range(n_tok):
-            ref = O.deltanet_layer_step(cs, S, proj_f[i, t], conv_w, dtb, a, nw)
-            what = f"in {in_dtype} out {out_dtype} seq {i} tok {t}"
+            ref = O.deltanet_layer_step(cs, S, proj_f[i, t], conv_w, dtb, a, nw, fast=fast)
+            what = f"in {in_dtype} out {out_dtype} seq {i} tok {t} fast {fast}"
             if out_dtype == kvc.DTYPE_F32:
                 rel_close(out[i, t], ref, what)
             else:
@@ -328,3 +333,41 @@ def test_deltanet_rejects_rows_past_2gib(in_dtype, n_tok):
         assert np.isfinite(ob.download(np.float32, (NV * DV,))).all()
     for b_ in bufs + [ob]:
         b_.free()
+
+
+@pytest.mark.parametrize("n_tok", [1, 5, 37])
+def test_deltanet_exact_math_flag_matches_exact_oracle(n_tok):
+    """KVC_FLAG_EXACT_MATH: hardware exp / log / reciprocal instead of the
+    reference's Schraudolph forms, through all three kernels (1 token, the
+    blocked kernel, the matrix form), against the oracle's fast = 0."""
+    say(f"deltanet exact-math flag, {n_tok} tokens")
+    run_case(kvc.DTYPE_BF16, kvc.DTYPE_F32, n_tok=n_tok, n_seqs=2, seed=8100 + n_tok, exact=True)
+
+
+def test_deltanet_reference_and_exact_modes_differ():
+    """The default (reference) output is far from the exact-math oracle and
+    close to the reference-mode oracle: the fp32 bar tells the modes apart."""
+    say("deltanet reference vs exact mode, 1 token")
+    h = kvc.hip()
+    rng = np.random.default_rng(8200)
+    conv_w, dtb, a, nw = weights(8201)
+    with ctx_ssm() as ctx:
+        s = ctx.seq_create()
+        rb, cb = state_bufs(ctx, s, 0)
+        S = (0.05 * rng.standard_normal((NV, DV, DK))).astype(np.float32)
+        cw = rng.standard_normal((3, C)).astype(np.float32)
+        rb.upload(S)
+        cb.upload(cw)
+        proj = rng.standard_normal(PROJ).astype(np.float32)
+        bufs = [kvc.to_device(x_) for x_ in (proj, conv_w, dtb, a, nw)]
+        ob = h.malloc(NV * DV * 4)
+        ctx.deltanet_step(0, [s], 1, bufs[0], bufs[1], bufs[2], bufs[3], bufs[4], ob, in_dtype=kvc.DTYPE_F32)
+        ctx.sync()
+        out = ob.download(np.float32, (NV * DV,))
+        for b_ in bufs + [ob]:
+            b_.free()
+    ref = O.deltanet_layer_step(cw.copy(), S.copy(), proj, conv_w, dtb, a, nw, fast=1)
+    exact = O.deltanet_layer_step(cw.copy(), S.copy(), proj, conv_w, dtb, a, nw, fast=0)
+    rel_close(out, ref, "reference mode")
+    d = out.astype(np.float64) - exact
+    assert np.sqrt((d ** 2).mean() / (exact.astype(np.float64) ** 2).mean()) > 1e-4

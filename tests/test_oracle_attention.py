@@ -17,12 +17,23 @@ def rand_case(L, seed, scale=1.0):
     return q, k, v
 
 
+@pytest.mark.parametrize("gate_mode", [0, 1])
 @pytest.mark.parametrize("L", [1, 33, 257])
-def test_decode_matches_golden(golden_dir, L):
+def test_decode_matches_golden(golden_dir, L, gate_mode):
     g = np.load(golden_dir / "attention_golden.npz")
     gate = g[f"dec{L}_gate"] if f"dec{L}_gate" in g else None
-    out = O.decode_attn(g[f"dec{L}_q"], g[f"dec{L}_k"], g[f"dec{L}_v"], L, gate=gate)
-    np.testing.assert_allclose(out, g[f"dec{L}_out"], rtol=0, atol=2e-5)
+    out = O.decode_attn(g[f"dec{L}_q"], g[f"dec{L}_k"], g[f"dec{L}_v"], L, gate=gate, gate_mode=gate_mode)
+    want = g[f"dec{L}_out_refgate"] if gate is not None and gate_mode == 1 else g[f"dec{L}_out"]
+    np.testing.assert_allclose(out, want, rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("gate_mode", [0, 1])
+def test_gated_decode_l1_matches_golden(golden_dir, gate_mode):
+    g = np.load(golden_dir / "attention_golden.npz")
+    out = O.decode_attn(g["g1_q"], g["g1_k"], g["g1_v"], 1, gate=g["g1_gate"], gate_mode=gate_mode)
+    want = g["g1_out_refgate"] if gate_mode == 1 else g["g1_out"]
+    # L = 1: out = v0 * sigma(gate), exact to fp32 rounding of one product
+    np.testing.assert_allclose(out, want, rtol=2e-7, atol=0)
 
 
 def test_prefill_matches_golden(golden_dir):
@@ -30,6 +41,13 @@ def test_prefill_matches_golden(golden_dir):
     pos0, n = int(g["pre_pos0"]), int(g["pre_n"])
     out = O.prefill_attn(g["pre_q"], g["pre_k"], g["pre_v"], pos0, n)
     np.testing.assert_allclose(out, g["pre_out"], rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("gate_mode", [0, 1])
+def test_gated_prefill_matches_golden(golden_dir, gate_mode):
+    g = np.load(golden_dir / "attention_golden.npz")
+    out = O.prefill_attn(g["pg_q"], g["pg_k"], g["pg_v"], 0, 8, gate=g["pg_gate"], gate_mode=gate_mode)
+    np.testing.assert_allclose(out, g["pg_out_refgate"] if gate_mode == 1 else g["pg_out"], rtol=0, atol=2e-5)
 
 
 @pytest.mark.parametrize("L,seed", [(5, 1), (64, 2), (300, 3), (1000, 4)])
@@ -100,12 +118,14 @@ def test_gate_multiplies_by_sigmoid():
     q, k, v = rand_case(L, 13)
     gate = O.normal_bf16(NQ * D, 14)
     plain = O.decode_attn(q, k, v, L)
-    gated = O.decode_attn(q, k, v, L, gate=gate)
+    gated = O.decode_attn(q, k, v, L, gate=gate, gate_mode=0)
     sg = 1 / (1 + np.exp(-O.bf16_to_f32(gate).astype(np.float64).reshape(NQ, D)))
     np.testing.assert_allclose(gated, plain * sg, rtol=1e-6, atol=1e-7)
-    # reference-compatible Schraudolph gate stays within its approximation error
+    # reference mode: the output is the ungated fp32 output times the exact
+    # model of fast_sigmoidf, one fp32 product per element, bit for bit
     ref_mode = O.decode_attn(q, k, v, L, gate=gate, gate_mode=1)
-    np.testing.assert_allclose(ref_mode, gated, atol=5e-2 * np.abs(plain).max())
+    sref = np.array([O.sigmoid_ref_model(float(x)) for x in O.bf16_to_f32(gate)], np.float32).reshape(NQ, D)
+    assert np.array_equal(ref_mode, plain * sref)
 
 
 def test_prefill_is_causal():

@@ -109,3 +109,42 @@ def test_schraudolph_exp():
     for x in (-8.0, -1.0, 0.0, 0.5, 3.0):
         assert abs(sig(x, 0) - 1 / (1 + math.exp(-x))) < 1e-6
         assert abs(sig(x, 1) - 1 / (1 + math.exp(-x))) < 2e-2
+
+
+def _bits(v):
+    return np.array([v], np.float32).view(np.uint32)[0]
+
+
+def test_schraudolph_exact_models_every_bf16_input():
+    """The oracle's reference-mode exp, sigmoid and SiLU equal the exact
+    rational model bit for bit for every finite bf16 input (the gate and the
+    conv / z activations of the path are bf16 or fp32 values)."""
+    L = O.L()
+    xs = O.finite_bf16_values()
+    fused_vs_unfused = 0
+    for x in xs.tolist():
+        assert _bits(L.orc_fast_expf(x)) == _bits(O.schraudolph_exp_model(x, rne=False)), x
+        assert _bits(L.orc_fast_expf_rne(x)) == _bits(O.schraudolph_exp_model(x, rne=True)), x
+        assert _bits(L.orc_sigmoid(x, 1)) == _bits(O.sigmoid_ref_model(x)), x
+        assert _bits(L.orc_silu(x, 1)) == _bits(O.silu_ref_model(x)), x
+        # the model discriminates: an unfused multiply-add (product rounded
+        # to fp32 first) gives another value for many inputs
+        xc = min(88.0, max(-88.0, x))
+        p = O.f32_round(O.Fraction(12102203) * O.Fraction(xc))
+        unfused = int(O.f32_round(O.Fraction(p) + 1065353216))
+        fused = int(O.f32_round(O.Fraction(12102203) * O.Fraction(xc) + 1065353216))
+        fused_vs_unfused += unfused != fused
+    assert fused_vs_unfused > 1000
+
+
+def test_schraudolph_exact_model_random_fp32():
+    L = O.L()
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([rng.standard_normal(10000) * 8, rng.uniform(-100, 100, 10000)]).astype(np.float32)
+    for x in xs.tolist():
+        assert _bits(L.orc_fast_expf(x)) == _bits(O.schraudolph_exp_model(x, rne=False)), x
+        assert _bits(L.orc_fast_expf_rne(x)) == _bits(O.schraudolph_exp_model(x, rne=True)), x
+    # RNE and truncation differ by at most one unit of the int pattern
+    for x in xs[:2000].tolist():
+        d = int(_bits(L.orc_fast_expf_rne(x))) - int(_bits(L.orc_fast_expf(x)))
+        assert d in (0, 1), x
