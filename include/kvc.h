@@ -207,6 +207,23 @@ int kvc_decode_attn(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
                     int32_t n_seqs, const void* q, const void* k_new,
                     const void* v_new, const void* gate, void* out,
                     int32_t out_dtype, float scale, void* stream);
+/* No counterpart in the reference.  kvc_decode_attn for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): same arguments, semantics and results
+ * (bit for bit: same work split and kernels), but the split-K partials and
+ * arrival counters live in the library's static per-GPU workspace -- a
+ * file-scope __device__ array of 2048 split-K items plus counters, 8.7 MB,
+ * held by each GPU the library runs on until the process ends -- instead of
+ * the context's.  The call allocates nothing.  A launch needing more than
+ * 2048 items (chunks x kv heads x output-dim parts) is refused with
+ * KVC_ERR_RANGE before anything runs; the automatic split stays within
+ * ~1100 items for 64 sequences of any length.  Every call on one GPU shares
+ * that workspace: calls that overlap on one GPU (other streams, other
+ * contexts, other host threads) race and must be serialised by the caller. */
+int kvc_decode_attn_static(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
+                           int32_t n_seqs, const void* q, const void* k_new,
+                           const void* v_new, const void* gate, void* out,
+                           int32_t out_dtype, float scale, void* stream);
 /* Causal chunked prefill.  The n_q query tokens of seq s sit at positions
  * [len_s + pending_s - n_q, len_s + pending_s) (their K/V appended already);
  * row i attends to keys [0, pos_i].  q/gate: bf16 [n_seqs][n_q][Hq][D];

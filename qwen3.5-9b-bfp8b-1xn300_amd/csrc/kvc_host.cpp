@@ -130,6 +130,8 @@ struct kvc_ctx {
     uint8_t* d_snap = nullptr;
     float* d_part = nullptr;
     int32_t* d_counters = nullptr;
+    float* s_part = nullptr;        // this device's static decode workspace
+    int32_t* s_counters = nullptr;  // (file-scope __device__ array, never freed)
     float* d_rope = nullptr;  // RoPE cos [max_seq_len][rope_dim/2], then sin likewise
 
     std::vector<int32_t> refcnt;
@@ -665,6 +667,13 @@ int kvc_create(const kvc_config* cfg, kvc_ctx** out) {
             delete c;
             return rc;
         }
+        // the static decode workspace of kvc_decode_attn_static: its device
+        // address on this GPU, looked up once per device
+        if ((e = (hipError_t)static_scratch(k.device, &c->s_part, &c->s_counters)) != hipSuccess) {
+            free_device(c);
+            delete c;
+            return hip_err(e, "static decode workspace");
+        }
     } else {
         if (k.pool_blocks <= 0 || k.pool_blocks > INT32_MAX) {
             delete c;
@@ -1087,8 +1096,84 @@ static int32_t auto_chunk_blocks(kvc_ctx* c, int64_t total_blocks) {
     return (int32_t)std::max<int64_t>(4, cb);
 }
 
-int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q, const void* k_new,
-                    const void* v_new, const void* gate, void* out, int32_t out_dtype, float scale, void* stream) {
+// Argument block of the decode launch over seqs[i0, i0 + n): work split and
+// pointers.  The split-K partials and arrival counters live in `part` /
+// `counters`; a launch needing more than `max_items` items is refused
+// (KVC_ERR_RANGE).  No allocation.
+static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t i0, int32_t n, const void* q,
+                             const void* k_new, const void* v_new, const void* gate, void* out, int32_t out_dtype,
+                             float scale, float* part, uint32_t part_bytes, int32_t* counters, int64_t max_items,
+                             const char* workspace, DecodeArgs& a) {
+    const size_t qrow = (size_t)kQHeads * kHeadDim, kvrow = (size_t)kKvHeads * kHeadDim;
+    const size_t osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
+    memset(&a, 0, sizeof a);
+    int64_t total_blocks = 0;
+    for (int32_t j = 0; j < n; j++) {
+        const Seq& s = c->seqs[seqs[i0 + j]];
+        const int32_t L = s.len + s.pending;
+        if (L <= 0) return set_err(KVC_ERR_STATE, "sequence %d has no keys to attend", seqs[i0 + j]);
+        if (k_new && s.pending < 1)
+            return set_err(KVC_ERR_STATE, "sequence %d: fused append needs a reserved token", seqs[i0 + j]);
+        a.slot[j] = seqs[i0 + j];
+        a.kv_len[j] = L;
+        total_blocks += (L + kBlockTok - 1) / kBlockTok;
+    }
+    int32_t cb = auto_chunk_blocks(c, total_blocks);
+    const bool force_split = c->cfg.flags & KVC_FLAG_DECODE_SPLIT_D;
+    const int64_t max_chunks = force_split ? kMaxChunks / kMaxDParts : kMaxChunks;
+    int64_t total_chunks;
+    for (;;) {
+        total_chunks = 0;
+        for (int32_t j = 0; j < n; j++) {
+            a.chunk_begin[j] = (int32_t)total_chunks;
+            const int32_t nb = (a.kv_len[j] + kBlockTok - 1) / kBlockTok;
+            total_chunks += (nb + cb - 1) / cb;
+        }
+        if (total_chunks <= max_chunks) break;
+        cb *= 2;
+    }
+    int32_t d_parts = 1;
+    if (force_split ||
+        (!(c->cfg.flags & KVC_FLAG_DECODE_NO_SPLIT_D) && total_chunks * kKvHeads < kDsplitBelowItems))
+        d_parts = 2;
+    const int64_t items = total_chunks * kKvHeads * d_parts;
+    if (items > max_items)
+        return set_err(KVC_ERR_RANGE,
+                       "decode of sequences %d..%d needs %lld split-K items; the %s holds %lld (use a larger "
+                       "decode_chunk_blocks or fewer sequences per call)",
+                       seqs[i0], seqs[i0 + n - 1], (long long)items, workspace, (long long)max_items);
+    a.chunk_begin[n] = (int32_t)total_chunks;
+    a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
+    a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
+    a.table = c->d_table;
+    a.q = static_cast<const uint16_t*>(q) + (size_t)i0 * qrow;
+    a.k_new = k_new ? static_cast<const uint16_t*>(k_new) + (size_t)i0 * kvrow : nullptr;
+    a.v_new = v_new ? static_cast<const uint16_t*>(v_new) + (size_t)i0 * kvrow : nullptr;
+    a.gate = gate ? static_cast<const uint16_t*>(gate) + (size_t)i0 * qrow : nullptr;
+    a.out = static_cast<uint8_t*>(out) + (size_t)i0 * qrow * osz;
+    a.part = part;
+    a.part_bytes = part_bytes;
+    a.counters = counters;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.out_bf16 = out_dtype == KVC_DTYPE_BF16;
+    a.table_stride = c->max_blocks;
+    a.n_seqs = n;
+    a.chunk_blocks = cb;
+    a.total_chunks = (int32_t)total_chunks;
+    a.d_parts = d_parts;
+    a.gate_ref = !(c->cfg.flags & KVC_FLAG_EXACT_MATH);
+    a.n_items = (int32_t)items;
+    a.per_xcd = (a.n_items + 7) / 8;
+    return KVC_OK;
+}
+
+// Decode over all seqs, 64 per launch; every launch is validated before the
+// first one is made.  Launches of one call run in stream order and share the
+// workspace.
+static int decode_impl(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q,
+                       const void* k_new, const void* v_new, const void* gate, void* out, int32_t out_dtype,
+                       float scale, void* stream, float* part, uint32_t part_bytes, int32_t* counters,
+                       int64_t max_items, const char* workspace) {
     if (!c) return set_err(KVC_ERR_INVALID, "null context");
     int rc;
     if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
@@ -1096,65 +1181,36 @@ int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
     if ((k_new == nullptr) != (v_new == nullptr)) return set_err(KVC_ERR_INVALID, "k_new and v_new go together");
     if (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16) return set_err(KVC_ERR_INVALID, "bad out_dtype");
     if (!std::isfinite(scale)) return set_err(KVC_ERR_INVALID, "scale must be finite");
-    const size_t qrow = (size_t)kQHeads * kHeadDim, kvrow = (size_t)kKvHeads * kHeadDim;
-    const size_t osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
-    for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
-        const int32_t n = std::min(kMaxBatch, n_seqs - i0);
-        DecodeArgs a{};
-        int64_t total_blocks = 0;
-        for (int32_t j = 0; j < n; j++) {
-            const Seq& s = c->seqs[seqs[i0 + j]];
-            const int32_t L = s.len + s.pending;
-            if (L <= 0) return set_err(KVC_ERR_STATE, "sequence %d has no keys to attend", seqs[i0 + j]);
-            if (k_new && s.pending < 1)
-                return set_err(KVC_ERR_STATE, "sequence %d: fused append needs a reserved token", seqs[i0 + j]);
-            a.slot[j] = seqs[i0 + j];
-            a.kv_len[j] = L;
-            total_blocks += (L + kBlockTok - 1) / kBlockTok;
-        }
-        int32_t cb = auto_chunk_blocks(c, total_blocks);
-        const bool force_split = c->cfg.flags & KVC_FLAG_DECODE_SPLIT_D;
-        const int64_t max_chunks = force_split ? kMaxChunks / kMaxDParts : kMaxChunks;
-        int64_t total_chunks;
-        for (;;) {
-            total_chunks = 0;
-            for (int32_t j = 0; j < n; j++) {
-                a.chunk_begin[j] = (int32_t)total_chunks;
-                const int32_t nb = (a.kv_len[j] + kBlockTok - 1) / kBlockTok;
-                total_chunks += (nb + cb - 1) / cb;
+    if (!part || !counters) return set_err(KVC_ERR_STATE, "no %s", workspace);
+    DecodeArgs a;
+    for (int pass = 0; pass < 2; pass++) {
+        for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+            const int32_t n = std::min(kMaxBatch, n_seqs - i0);
+            if ((rc = build_decode_args(c, layer, seqs, i0, n, q, k_new, v_new, gate, out, out_dtype, scale, part,
+                                        part_bytes, counters, max_items, workspace, a)))
+                return rc;
+            if (pass == 1) {
+                int e = launch_decode(a, stream);
+                if (e) return hip_err((hipError_t)e, "decode launch");
             }
-            if (total_chunks <= max_chunks) break;
-            cb *= 2;
         }
-        int32_t d_parts = 1;
-        if (force_split ||
-            (!(c->cfg.flags & KVC_FLAG_DECODE_NO_SPLIT_D) && total_chunks * kKvHeads < kDsplitBelowItems))
-            d_parts = 2;
-        a.chunk_begin[n] = (int32_t)total_chunks;
-        a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
-        a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
-        a.table = c->d_table;
-        a.q = static_cast<const uint16_t*>(q) + (size_t)i0 * qrow;
-        a.k_new = k_new ? static_cast<const uint16_t*>(k_new) + (size_t)i0 * kvrow : nullptr;
-        a.v_new = v_new ? static_cast<const uint16_t*>(v_new) + (size_t)i0 * kvrow : nullptr;
-        a.gate = gate ? static_cast<const uint16_t*>(gate) + (size_t)i0 * qrow : nullptr;
-        a.out = static_cast<uint8_t*>(out) + (size_t)i0 * qrow * osz;
-        a.part = c->d_part;
-        a.counters = c->d_counters;
-        a.scale_log2 = scale * 1.4426950408889634f;
-        a.out_bf16 = out_dtype == KVC_DTYPE_BF16;
-        a.table_stride = c->max_blocks;
-        a.n_seqs = n;
-        a.chunk_blocks = cb;
-        a.total_chunks = (int32_t)total_chunks;
-        a.d_parts = d_parts;
-        a.gate_ref = !(c->cfg.flags & KVC_FLAG_EXACT_MATH);
-        a.n_items = (int32_t)(total_chunks * kKvHeads * d_parts);
-        a.per_xcd = (a.n_items + 7) / 8;
-        int e = launch_decode(a, stream);
-        if (e) return hip_err((hipError_t)e, "decode launch");
     }
     return KVC_OK;
+}
+
+int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q, const void* k_new,
+                    const void* v_new, const void* gate, void* out, int32_t out_dtype, float scale, void* stream) {
+    return decode_impl(c, layer, seqs, n_seqs, q, k_new, v_new, gate, out, out_dtype, scale, stream,
+                       c ? c->d_part : nullptr, (uint32_t)kPartBytes, c ? c->d_counters : nullptr,
+                       (int64_t)kMaxChunks * kKvHeads, "context's split-K workspace");
+}
+
+int kvc_decode_attn_static(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q,
+                           const void* k_new, const void* v_new, const void* gate, void* out, int32_t out_dtype,
+                           float scale, void* stream) {
+    return decode_impl(c, layer, seqs, n_seqs, q, k_new, v_new, gate, out, out_dtype, scale, stream,
+                       c ? c->s_part : nullptr, (uint32_t)kStaticPartBytes, c ? c->s_counters : nullptr,
+                       kStaticItems, "static decode workspace");
 }
 
 int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t n_q, const void* q,

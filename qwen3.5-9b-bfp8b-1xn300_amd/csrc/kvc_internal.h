@@ -39,6 +39,13 @@ constexpr int kItemFloats = 1056;
 constexpr int kMaxDParts = 2;        // output-dim parts per decode chunk
 constexpr int kCounterStride = 32;   // int32s between arrival counters (one 128-B line each)
 constexpr size_t kPartBytes = (size_t)kMaxChunks * kKvHeads * kItemFloats * 4;
+constexpr size_t kCounterBytes = (size_t)kMaxBatch * kKvHeads * kMaxDParts * kCounterStride * 4;
+// Static workspace of kvc_decode_attn_static, the entry point that allocates
+// nothing: a file-scope __device__ array of this many split-K items (plus the
+// arrival counters) per GPU, held until the process ends.
+constexpr int kStaticItems = 2048;
+constexpr size_t kStaticPartBytes = (size_t)kStaticItems * kItemFloats * 4;  // 8,650,752 B
+constexpr int kMaxDevices = 64;
 constexpr int kTableUpdatesPerLaunch = 480;
 
 // ---- kernel argument blocks (passed by value; must stay < 4 KiB) ----------
@@ -61,6 +68,8 @@ struct DecodeArgs {
     const uint16_t* gate;   // [n_seqs][Hq][D] or null
     void* out;              // [n_seqs][Hq][D]
     float* part;            // split-K workspace [item][G][D + 2]
+    uint32_t part_bytes;    // its size (bound of the buffer resource)
+    int32_t pad0;
     int32_t* counters;      // [kMaxBatch][Hkv][kMaxDParts] arrival counters, kCounterStride
                             // apart (self-resetting)
     float scale_log2;       // scale * log2(e)
@@ -227,6 +236,12 @@ struct BlockCopyArgs {
 };
 
 // ---- launchers (kvc_kernels.hip); return hipError_t as int ---------------
+// Device address of this GPU's static decode workspace (split-K partials,
+// then the arrival counters), looked up once per device with
+// hipGetSymbolAddress and its counters zeroed then; `device` must be current.
+// Returns a hipError_t.
+int static_scratch(int device, float** part, int32_t** counters);
+
 int launch_table_update(const TableUpdateArgs& a, void* stream);
 int launch_decode(const DecodeArgs& a, void* stream);
 int launch_append(const AppendArgs& a, void* stream);

@@ -5,6 +5,7 @@
 // All K/V traffic is bf16; arithmetic is fp32 (v_dot2_f32_bf16 for q.k).
 // Softmax runs in the log2 domain: s2 = (q.k) * scale * log2(e), p = 2^(s2-m).
 #include <atomic>
+#include <mutex>
 #include "kvc_device.h"
 #include "kvc_internal.h"
 
@@ -637,7 +638,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     // publish (m, l, acc) with agent-coherent 16-B stores; once they have all
     // completed (s_waitcnt 0) the arrival counter is bumped.  The last item of
     // (s, h, part) to arrive reads the partials back with agent-coherent loads.
-    const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.part, (uint32_t)kPartBytes);
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.part, a.part_bytes);
     const int ibase = item * kItemFloats * 4;
     const int aoff = g * kHeadDim + (d0 - dpart * (kHeadDim / NP));  // acc slot of this thread's dims
     if (act) {
@@ -2470,6 +2471,44 @@ __global__ __launch_bounds__(256) void fill_normal_kernel(uint16_t* dst, int64_t
 int launch_table_update(const TableUpdateArgs& a, void* stream) {
     hipLaunchKernelGGL(table_update_kernel, dim3(1), dim3(512), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Static decode workspace for kvc_decode_attn_static: split-K partials of up
+// to kStaticItems items, then the arrival counters.  Each GPU the library runs
+// on holds its own copy until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol):
+// the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) uint8_t scratch[kStaticPartBytes + kCounterBytes];
+
+__global__ __launch_bounds__(256) void zero_words_kernel(int32_t* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+namespace {
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int static_scratch(int device, float** part, int32_t** counters) {
+    if (device < 0 || device >= kMaxDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        // the counters must start at zero (the kernels reset them after use);
+        // a fill kernel, not a memset, in case a caller captures later work
+        int32_t* ctr = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(ptr) + kStaticPartBytes);
+        const int n = (int)(kCounterBytes / 4);
+        hipLaunchKernelGGL(zero_words_kernel, dim3((n + 255) / 256), dim3(256), 0, nullptr, ctr, n);
+        if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(nullptr)) != hipSuccess) return (int)e;
+        g_scratch_ptr[device] = static_cast<uint8_t*>(ptr);
+    }
+    *part = reinterpret_cast<float*>(g_scratch_ptr[device]);
+    *counters = reinterpret_cast<int32_t*>(g_scratch_ptr[device] + kStaticPartBytes);
+    return (int)hipSuccess;
 }
 
 int launch_decode(const DecodeArgs& a, void* stream) {

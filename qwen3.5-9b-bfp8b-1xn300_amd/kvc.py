@@ -43,7 +43,7 @@ EXPORTS = [
     "kvc_get_stats", "kvc_abi_version", "kvc_seq_create", "kvc_seq_release",
     "kvc_seq_reset", "kvc_seq_len", "kvc_seq_truncate", "kvc_seq_reserve",
     "kvc_seq_commit", "kvc_prefix_match", "kvc_append", "kvc_qkv_append", "kvc_decode_attn",
-    "kvc_prefill_attn", "kvc_gather", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
+    "kvc_decode_attn_static", "kvc_prefill_attn", "kvc_gather", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
     "kvc_snapshot_restore", "kvc_snapshot_release", "kvc_pool_fill_normal",
     "kvc_fill_normal_bf16", "kvc_sync",
 ]
@@ -113,6 +113,7 @@ def lib() -> ctypes.CDLL:
             "kvc_append": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P]),
             "kvc_qkv_append": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, P, P]),
             "kvc_decode_attn": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
+            "kvc_decode_attn_static": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
             "kvc_prefill_attn": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P, I32, F32, P]),
             "kvc_gather": (ctypes.c_int, [P, I32, pI32, I32, I32, pI32, P, P, P]),
             "kvc_state_ptrs": (ctypes.c_int, [P, I32, I32, ctypes.POINTER(P), ctypes.POINTER(P)]),
@@ -377,6 +378,13 @@ class Context:
         _check(self.L.kvc_decode_attn(self.ptr, layer, _i32(seqs), len(seqs), self._p(q), self._p(k_new),
                                       self._p(v_new), self._p(gate), self._p(out), out_dtype,
                                       ctypes.c_float(scale), stream))
+
+    def decode_attn_static(self, layer, seqs, q, out, k_new=None, v_new=None, gate=None,
+                           out_dtype=DTYPE_F32, scale=1.0 / 16, stream=None):
+        """decode_attn on the library's static per-GPU workspace (allocates nothing)"""
+        _check(self.L.kvc_decode_attn_static(self.ptr, layer, _i32(seqs), len(seqs), self._p(q), self._p(k_new),
+                                             self._p(v_new), self._p(gate), self._p(out), out_dtype,
+                                             ctypes.c_float(scale), stream))
 
     def prefill_attn(self, layer, seqs, n_q, q, out, gate=None, out_dtype=DTYPE_F32,
                      scale=1.0 / 16, stream=None):
