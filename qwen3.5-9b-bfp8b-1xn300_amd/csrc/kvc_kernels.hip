@@ -711,9 +711,19 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
             Lc = fmaf(Lc, cs, wave_sum(w_l * __uint_as_float(ml[1])));
 #pragma unroll
             for (int j = 0; j < 4; j++) Ac[j] *= cs;
+            // both halves' weights are read for every lane and selected per
+            // lane: a readlane under a lane-dependent condition is compiled
+            // as a divergent branch per partial (measured: 0.7 us per launch
+            // at config b)
+            float we[kNB], wo[kNB];
 #pragma unroll
             for (int k = 0; k < kNB; k++) {
-                const float w = psub ? readlane(w_l, k * NP + 1) : readlane(w_l, k * NP);
+                we[k] = readlane(w_l, k * NP);
+                wo[k] = readlane(w_l, k * NP + 1);
+            }
+#pragma unroll
+            for (int k = 0; k < kNB; k++) {
+                const float w = psub ? wo[k] : we[k];
 #pragma unroll
                 for (int j = 0; j < 4; j++) Ac[j] = fmaf(w, __uint_as_float(pa[k][j]), Ac[j]);
             }
