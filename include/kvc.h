@@ -212,7 +212,7 @@ int kvc_decode_attn(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
  * harnesses that forbid hipMalloc): same arguments, semantics and results
  * (bit for bit: same work split and kernels), but the split-K partials and
  * arrival counters live in the library's static per-GPU workspace -- a
- * file-scope __device__ array of 2048 split-K items plus counters, 8.7 MB,
+ * file-scope __device__ array of 2048 split-K items plus counters, 8.9 MB,
  * held by each GPU the library runs on until the process ends -- instead of
  * the context's.  The call allocates nothing.  A launch needing more than
  * 2048 items (chunks x kv heads x output-dim parts) is refused with

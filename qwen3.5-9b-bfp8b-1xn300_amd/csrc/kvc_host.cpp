@@ -620,7 +620,7 @@ int kvc_create(const kvc_config* cfg, kvc_ctx** out) {
         }
         const size_t table_bytes = (size_t)k.max_seqs * c->max_blocks * 4;
         const size_t part_bytes = kPartBytes;
-        const size_t ctr_bytes = (size_t)kMaxBatch * kKvHeads * kMaxDParts * kCounterStride * 4;
+        const size_t ctr_bytes = kCounterBytes;
         if ((rc = dev_alloc(c, (void**)&c->d_table, table_bytes, "block table")) ||
             (rc = dev_alloc(c, (void**)&c->d_state, (size_t)c->state_bytes * k.max_seqs, "state pool")) ||
             (rc = dev_alloc(c, (void**)&c->d_snap, (size_t)c->snap_bytes * n_snap, "snapshot pool")) ||

@@ -39,12 +39,13 @@ constexpr int kItemFloats = 1056;
 constexpr int kMaxDParts = 2;        // output-dim parts per decode chunk
 constexpr int kCounterStride = 32;   // int32s between arrival counters (one 128-B line each)
 constexpr size_t kPartBytes = (size_t)kMaxChunks * kKvHeads * kItemFloats * 4;
-constexpr size_t kCounterBytes = (size_t)kMaxBatch * kKvHeads * kMaxDParts * kCounterStride * 4;
+// one arrival counter per (sequence, kv head, output-dim part, q head of the group)
+constexpr size_t kCounterBytes = (size_t)kMaxBatch * kKvHeads * kMaxDParts * kGroup * kCounterStride * 4;
 // Static workspace of kvc_decode_attn_static, the entry point that allocates
 // nothing: a file-scope __device__ array of this many split-K items (plus the
 // arrival counters) per GPU, held until the process ends.
 constexpr int kStaticItems = 2048;
-constexpr size_t kStaticPartBytes = (size_t)kStaticItems * kItemFloats * 4;  // 8,650,752 B
+constexpr size_t kStaticPartBytes = (size_t)kStaticItems * kItemFloats * 4;  // 8,650,752 B (+ 256 KiB counters)
 constexpr int kMaxDevices = 64;
 constexpr int kTableUpdatesPerLaunch = 480;
 
@@ -70,7 +71,7 @@ struct DecodeArgs {
     float* part;            // split-K workspace [item][G][D + 2]
     uint32_t part_bytes;    // its size (bound of the buffer resource)
     int32_t pad0;
-    int32_t* counters;      // [kMaxBatch][Hkv][kMaxDParts] arrival counters, kCounterStride
+    int32_t* counters;      // [kMaxBatch][Hkv][kMaxDParts][G] arrival counters, kCounterStride
                             // apart (self-resetting)
     float scale_log2;       // scale * log2(e)
     int32_t out_bf16;

@@ -635,9 +635,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
         if (act) write_out(a.out, a.out_bf16, orow, d0, grow, a.gate_ref, Lsum, A);
         return;
     }
-    // publish (m, l, acc) with agent-coherent 16-B stores; once they have all
-    // completed (s_waitcnt 0) the arrival counter is bumped.  The last item of
-    // (s, h, part) to arrive reads the partials back with agent-coherent loads.
+    // Wave g publishes q head g's (m, l, acc) with agent-coherent stores;
+    // once they have completed (its own s_waitcnt 0) it bumps head g's
+    // arrival counter.  The last wave to arrive for (s, h, part, g) reads the
+    // partials back with agent-coherent loads and writes head g's output.
+    // Each wave arrives on its own: no workgroup barrier and no LDS
+    // broadcast of the arrival lie on the path to the combine.
     const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.part, a.part_bytes);
     const int ibase = item * kItemFloats * 4;
     const int aoff = g * kHeadDim + (d0 - dpart * (kHeadDim / NP));  // acc slot of this thread's dims
@@ -649,23 +652,19 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
         av[3] = __float_as_uint(A[3]);
         __builtin_amdgcn_raw_buffer_store_b128(av, prs, ibase + aoff * 4, 0, kCpolSC1);
     }
-    if ((t & 63) == 0) {
+    if (lane == 0) {
         u32x2 mlv;
         mlv[0] = __float_as_uint(M);
         mlv[1] = __float_as_uint(Lsum);
         __builtin_amdgcn_raw_buffer_store_b64(mlv, prs, ibase + (kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
     }
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
     // one 128-B line per counter: arrivals on different counters do not
     // contend for one line
-    int32_t* ctr = a.counters + ((s * kKvHeads + h) * kMaxDParts + dpart) * kCounterStride;
-    if (t == 0) {
-        const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        sm.last = (prev == n_chunks - 1);
-    }
-    __syncthreads();
-    if (!sm.last) return;
+    int32_t* ctr = a.counters + (((s * kKvHeads + h) * kMaxDParts + dpart) * kGroup + g) * kCounterStride;
+    int prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__builtin_amdgcn_readfirstlane(prev) != n_chunks - 1) return;
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (NP == 1) {
         // combine the n_chunks partials of (s, h): wave g takes q head g; every
@@ -732,7 +731,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
         for (int j = 0; j < 4; j++) Ac[j] = sum_xor32(Ac[j]);
     }
     if (act) write_out(a.out, a.out_bf16, orow, d0, grow, a.gate_ref, Lc, Ac);
-    if (t == 0) *ctr = 0;
+    if (lane == 0) *ctr = 0;
 }
 
 // ---------------------------------------------------------------------------

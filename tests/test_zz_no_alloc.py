@@ -1,7 +1,7 @@
 """kvc_decode_attn_static: decode attention that allocates nothing, for
 callers that cannot call hipMalloc (HIP graph capture, tight serving loops).
 Its split-K partials and arrival counters live in a file-scope __device__
-array of the library (kStaticItems = 2048 items, 8.7 MB per GPU) instead of
+array of the library (kStaticItems = 2048 items plus counters, 8.9 MB per GPU) instead of
 the context's workspace.  Through the C ABI, on two calls in a row (the
 second smaller), its output must equal kvc_decode_attn's bit for bit: both
 take the same work split and kernels.  A call that needs more split-K items
