@@ -113,71 +113,109 @@ def cpu_baseline_b(L=4096, budget_s=12.0):
     return res, cores
 
 
-def run_b(args):
-    import kvc
+class DecodeB:
+    """Config b exactly as benched: one sequence per cache replica at L - 1
+    tokens, 8 layers, fused 1-token append + decode per layer (automatic
+    chunk and output-dim split), bf16 output.  One HIP graph holds a round of
+    `reps` steps (step r decodes replica r; kernel arguments carry each
+    sequence's length); one graph per replica serves the steps left over when
+    K is not a multiple of reps.  Per round the host reserves the appended
+    slot of every replica in one call, replays the graph, commits in one call
+    and truncates each replica back to L - 1, so every step overwrites slot
+    L - 1 and L stays 4096.  Batching the bookkeeping per round keeps the
+    Python host loop ahead of the GPU.  tests/test_gpu_bench_b.py checks
+    these launches against the oracle."""
 
-    h = kvc.hip()
-    if h.device_count() < 1:
-        raise RuntimeError("no HIP device visible")
-    L, layers, reps = 4096, 8, args.replicas
-    blocks_per_seq = L // BT
-    ctx = kvc.Context(n_attn_layers=layers, n_ssm_layers=0, max_seqs=max(reps, 4), max_seq_len=L + 64,
-                      pool_blocks=reps * (blocks_per_seq + 2), snapshot_slots=0, alloc_seed=SEED + 2,
-                      decode_chunk_blocks=args.chunk_blocks)
-    stream = h.stream()
-    log(f"config b: {layers} layers, L={L}, {reps} replicas, pool fill")
-    ctx.pool_fill_normal(SEED + 2, stream)
-    seqs = [ctx.seq_create() for _ in range(reps)]
-    ctx.reserve(seqs, L - 1, stream)
-    ctx.commit(seqs, L - 1, None, stream)
-    q = h.malloc(reps * layers * NQ * D * 2)
-    kn = h.malloc(reps * layers * ROW * 2)
-    vn = h.malloc(reps * layers * ROW * 2)
-    out = h.malloc(reps * layers * NQ * D * 2)
-    ctx.fill_normal_bf16(q, reps * layers * NQ * D, SEED + 4, 1.0, stream)
-    ctx.fill_normal_bf16(kn, reps * layers * ROW, SEED + 5, 1.0, stream)
-    ctx.fill_normal_bf16(vn, reps * layers * ROW, SEED + 6, 1.0, stream)
-    h.stream_sync(stream)
+    def __init__(self, reps=4, chunk_blocks=0, L=4096, layers=8):
+        import kvc
 
-    def enqueue_step(r):
-        for layer in range(layers):
-            i = r * layers + layer
-            ctx.decode_attn(layer, [seqs[r]], q.ptr + i * NQ * D * 2, out.ptr + i * NQ * D * 2,
-                            k_new=kn.ptr + i * ROW * 2, v_new=vn.ptr + i * ROW * 2,
-                            out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
+        self.kvc = kvc
+        h = self.h = kvc.hip()
+        if h.device_count() < 1:
+            raise RuntimeError("no HIP device visible")
+        self.L, self.layers, self.reps = L, layers, reps
+        ctx = self.ctx = kvc.Context(n_attn_layers=layers, n_ssm_layers=0, max_seqs=max(reps, 4),
+                                     max_seq_len=L + 64, pool_blocks=reps * (L // BT + 2), snapshot_slots=0,
+                                     alloc_seed=SEED + 2, decode_chunk_blocks=chunk_blocks)
+        stream = self.stream = h.stream()
+        ctx.pool_fill_normal(SEED + 2, stream)
+        seqs = self.seqs = [ctx.seq_create() for _ in range(reps)]
+        ctx.reserve(seqs, L - 1, stream)
+        ctx.commit(seqs, L - 1, None, stream)
+        n = reps * layers
+        self.q = h.malloc(n * NQ * D * 2)
+        self.kn = h.malloc(n * ROW * 2)
+        self.vn = h.malloc(n * ROW * 2)
+        self.out = h.malloc(n * NQ * D * 2)
+        self.sums = h.malloc(8 * n * (L // BT) * 2 * NKV)  # per-unit checksums of each (replica, layer)
+        ctx.fill_normal_bf16(self.q, n * NQ * D, SEED + 4, 1.0, stream)
+        ctx.fill_normal_bf16(self.kn, n * ROW, SEED + 5, 1.0, stream)
+        ctx.fill_normal_bf16(self.vn, n * ROW, SEED + 6, 1.0, stream)
+        h.stream_sync(stream)
+        ctx.reserve(seqs, 1, stream)
+        self.graph = h.capture(stream, lambda: [self.enqueue_step(r) for r in range(reps)])
+        self.single = [h.capture(stream, lambda r=r: self.enqueue_step(r)) for r in range(reps)]
+        # the read floor: the same replicas' K/V read once per layer by the
+        # checksum kernel (whole blocks, no arithmetic to speak of)
+        self.floor_graph = h.capture(stream, lambda: [self.enqueue_floor(r) for r in range(reps)])
+        ctx.commit(seqs, 1, None, stream)
+        for s_ in seqs:
+            ctx.seq_truncate(s_, L - 1)
 
-    # One graph holds a round of reps steps (step r decodes replica r; kernel
-    # arguments carry each sequence's length); one graph per replica serves the
-    # steps left over when K is not a multiple of reps.  Per round the host
-    # reserves the appended slot of every replica in one call, replays the
-    # graph, commits in one call and truncates each replica back to L-1, so
-    # every step overwrites slot L-1 and L stays 4096.  Batching the
-    # bookkeeping per round keeps the Python host loop ahead of the GPU.
-    def enqueue_round():
-        for r in range(reps):
-            enqueue_step(r)
+    def enqueue_step(self, r):
+        for layer in range(self.layers):
+            i = r * self.layers + layer
+            self.ctx.decode_attn(layer, [self.seqs[r]], self.q.ptr + i * NQ * D * 2, self.out.ptr + i * NQ * D * 2,
+                                 k_new=self.kn.ptr + i * ROW * 2, v_new=self.vn.ptr + i * ROW * 2,
+                                 out_dtype=self.kvc.DTYPE_BF16, scale=1.0 / 16, stream=self.stream)
 
-    ctx.reserve(seqs, 1, stream)
-    graph = h.capture(stream, enqueue_round)
-    single = [h.capture(stream, lambda r=r: enqueue_step(r)) for r in range(reps)]
-    ctx.commit(seqs, 1, None, stream)
-    for s_ in seqs:
-        ctx.seq_truncate(s_, L - 1)
+    def enqueue_floor(self, r):
+        per = (self.L // BT) * 2 * NKV
+        for layer in range(self.layers):
+            i = r * self.layers + layer
+            self.ctx.kv_checksum(layer, [self.seqs[r]], self.sums.ptr + 8 * i * per, stream=self.stream)
 
-    def run_steps(n):
+    def begin_round(self, seqs=None):
+        self.ctx.reserve(self.seqs if seqs is None else seqs, 1, self.stream)
+
+    def end_round(self, seqs=None):
+        seqs = self.seqs if seqs is None else seqs
+        self.ctx.commit(seqs, 1, None, self.stream)
+        for s_ in seqs:
+            self.ctx.seq_truncate(s_, self.L - 1)
+
+    def run_steps(self, n):
         """n steps: whole rounds from the round graph, the rest one by one."""
-        for _ in range(n // reps):
-            ctx.reserve(seqs, 1, stream)
-            h.graph_launch(graph, stream)
-            ctx.commit(seqs, 1, None, stream)
-            for s_ in seqs:
-                ctx.seq_truncate(s_, L - 1)
-        for r in range(n % reps):
-            ctx.reserve([seqs[r]], 1, stream)
-            h.graph_launch(single[r], stream)
-            ctx.commit([seqs[r]], 1, None, stream)
-            ctx.seq_truncate(seqs[r], L - 1)
+        h = self.h
+        for _ in range(n // self.reps):
+            self.begin_round()
+            h.graph_launch(self.graph, self.stream)
+            self.end_round()
+        for r in range(n % self.reps):
+            self.begin_round([self.seqs[r]])
+            h.graph_launch(self.single[r], self.stream)
+            self.end_round([self.seqs[r]])
 
+    def run_floor(self, rounds):
+        """rounds x reps x layers checksum launches over the 4096-key caches."""
+        self.ctx.reserve(self.seqs, 1, self.stream)  # the checksums cover L keys, like the decode
+        for _ in range(rounds):
+            self.h.graph_launch(self.floor_graph, self.stream)
+        self.end_round()
+
+    def close(self):
+        for g_ in [self.graph, self.floor_graph] + self.single:
+            self.h.graph_destroy(g_)
+        for b_ in (self.q, self.kn, self.vn, self.out, self.sums):
+            b_.free()
+        self.ctx.close()
+
+
+def run_b(args):
+    L, layers = 4096, 8
+    log(f"config b: {layers} layers, L={L}, {args.replicas} replicas, pool fill")
+    B = DecodeB(reps=args.replicas, chunk_blocks=args.chunk_blocks, L=L, layers=layers)
+    h, stream, run_steps, reps = B.h, B.stream, B.run_steps, B.reps
     steps = args.steps
     run_steps(args.warmup)
     h.stream_sync(stream)
@@ -198,11 +236,16 @@ def run_b(args):
     # rocprofv3 kernel-trace average of the same command).
     kern_us = us_layer
     achieved = bpl / (kern_us * 1e-6) / 1e9
-    for g_ in [graph] + single:
-        h.graph_destroy(g_)
-    for b_ in (q, kn, vn, out):
-        b_.free()
-    ctx.close()
+    # single-launch read floor: the checksum kernel reads the same 16 MiB of
+    # K/V per layer through the block table, in the same rotated graph setup
+    f_rounds = max(1, steps // (B.reps * 4))
+    B.run_floor(2)
+    h.stream_sync(stream)
+    h.record(e0, stream)
+    B.run_floor(f_rounds)
+    h.record(e1, stream)
+    floor_us = h.elapsed_ms(e0, e1) * 1e3 / (f_rounds * B.reps * layers)
+    B.close()
 
     line = {
         "metric": METRIC,
@@ -224,6 +267,10 @@ def run_b(args):
         "us_per_layer": round(us_layer, 3),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "bytes_per_layer": bpl,
+        "floor_us": round(floor_us, 3),
+        "floor_note": "one checksum_kernel launch reading the same 16 MiB of K/V (whole blocks) per layer, "
+                      "same graph and replica rotation: the single-launch read floor",
+        "pct_of_floor": round(100 * floor_us / us_layer, 1),
         "host_wall_us_per_step": round(wall * 1e6 / steps, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),

@@ -239,6 +239,19 @@ int kvc_gather(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
                int32_t n_seqs, int32_t tok0, const int32_t* n_tok,
                void* k_out, void* v_out, void* stream);
 
+/* Integrity checksums of each seq's cached K/V in one layer, one per 16-KiB
+ * (block, K|V, kv head) unit (no counterpart in the reference; a cheap check
+ * that a reused, restored or copied prefix holds the bytes it should, and
+ * which block does not).  out (device memory, uint64) receives, for each seq
+ * in order, ceil((len + pending) / 32) x 2 x Hkv entries ordered [block][K, V]
+ * [kv head]; entry = sum(w_j) in the low 32 bits and sum(w_j ^ j) in the
+ * high 32 bits, both mod 2^32, over the 32-bit words w_j of the unit's
+ * [token][d] rows (j = token * D/2 + word) for tokens below len + pending.
+ * Reads whole blocks and writes 8 B per unit: the bench's single-launch read
+ * floor and a counter calibration of known size. */
+int kvc_kv_checksum(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
+                    int32_t n_seqs, uint64_t* out, void* stream);
+
 /* ---- recurrent state + snapshots ---------------------------------------- */
 /* Live state of seq for Gated-DeltaNet layer ssm_layer: rec = fp32
  * [v_heads][v_dim][k_dim], conv = fp32 [conv_rows][conv_channels]. */

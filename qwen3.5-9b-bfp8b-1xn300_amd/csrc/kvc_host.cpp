@@ -1302,6 +1302,42 @@ int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
     return KVC_OK;
 }
 
+int kvc_kv_checksum(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, uint64_t* out, void* stream) {
+    if (!c) return set_err(KVC_ERR_INVALID, "null context");
+    int rc;
+    if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
+    if (!out) return set_err(KVC_ERR_INVALID, "checksum needs an output array");
+    int64_t out_off = 0;
+    for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
+        const int32_t n = std::min(kMaxBatch, n_seqs - i0);
+        ChecksumArgs a{};
+        int64_t units = 0;
+        for (int32_t j = 0; j < n; j++) {
+            const Seq& s = c->seqs[seqs[i0 + j]];
+            const int32_t L = s.len + s.pending;
+            a.slot[j] = seqs[i0 + j];
+            a.kv_len[j] = L;
+            a.unit_begin[j] = (int32_t)units;
+            units += (int64_t)((L + kBlockTok - 1) / kBlockTok) * 2 * kKvHeads;
+        }
+        a.unit_begin[n] = (int32_t)units;
+        if (units > INT32_MAX) return set_err(KVC_ERR_RANGE, "checksum too large");
+        a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
+        a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
+        a.table = c->d_table;
+        a.out = out + out_off;
+        a.table_stride = c->max_blocks;
+        a.n_seqs = n;
+        a.n_units = (int32_t)units;
+        if (units > 0) {
+            int e = launch_checksum(a, stream);
+            if (e) return hip_err((hipError_t)e, "checksum launch");
+        }
+        out_off += units;
+    }
+    return KVC_OK;
+}
+
 // ---- state + snapshots -------------------------------------------------------
 
 int kvc_state_ptrs(kvc_ctx* c, int32_t seq, int32_t ssm_layer, void** rec, void** conv) {

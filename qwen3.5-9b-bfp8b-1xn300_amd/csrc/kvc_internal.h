@@ -184,6 +184,21 @@ struct GatherArgs {
     int32_t item_begin[kMaxBatch + 1];  // first work item of each sequence
 };
 
+// K/V checksums: one work unit = one (block, K|V, kv head) unit of 16 KiB.
+struct ChecksumArgs {
+    const uint16_t* kpool;
+    const uint16_t* vpool;
+    const int32_t* table;
+    uint64_t* out;                       // one checksum per unit, units of all seqs back to back
+    int32_t table_stride;
+    int32_t n_seqs;
+    int32_t n_units;
+    int32_t pad;
+    int32_t slot[kMaxBatch];
+    int32_t kv_len[kMaxBatch];           // tokens covered
+    int32_t unit_begin[kMaxBatch + 1];   // first unit of each sequence (launch-relative)
+};
+
 struct PrefillArgs {
     const uint16_t* kpool;
     const uint16_t* vpool;
@@ -250,6 +265,7 @@ int launch_qkv_append(const QkvArgs& a, void* stream);
 int launch_deltanet(const DeltaNetArgs& a, void* stream);
 int launch_zero_state(const ZeroStateArgs& a, void* stream);
 int launch_gather(const GatherArgs& a, void* stream);
+int launch_checksum(const ChecksumArgs& a, void* stream);
 int launch_prefill(const PrefillArgs& a, void* stream);
 int launch_snapshot(const SnapshotArgs& a, void* stream);
 int launch_block_copy(const BlockCopyArgs& a, void* stream);

@@ -2393,6 +2393,71 @@ __device__ __forceinline__ int64_t snap_units_end(const SnapshotArgs& a) {
     const int64_t seg_bytes = (int64_t)a.n_layers * 2 * a.seg_blocks * (int64_t)kBlockBytes;
     return a.do_kv ? (a.state_bytes + seg_bytes) / 16 : a.state_bytes / 16;
 }
+// ---------------------------------------------------------------------------
+// K/V checksums, one per (block, K|V, kv head) unit of 16 KiB: one 256-thread
+// workgroup reads one unit, 4 x 16 B per thread, all loads issued before any
+// is used, and folds its 32-bit words w_j (j = token * 128 + word of the
+// 512-B head row) into two sums, sum(w_j) and sum(w_j ^ j); the second makes
+// the checksum depend on where each word sits.  Slots past the sequence end
+// are read (whole units stream best) but not summed.  No atomics and no
+// exchange between workgroups: each writes its unit's 8 bytes.  A
+// read-only kernel of exactly known size: the bench uses it as the
+// single-launch read floor of a decode's K/V and for counter calibration.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t x) {
+    x += __builtin_amdgcn_update_dpp(0u, x, kDppXor1, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, kDppXor2, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, kDppHalfMirror, 0xF, 0xF, false);
+    x += __builtin_amdgcn_update_dpp(0u, x, kDppRowRor8, 0xF, 0xF, false);
+    auto r16 = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = r16[0] + r16[1];
+    auto r32 = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return r32[0] + r32[1];
+}
+
+__global__ __launch_bounds__(256) void checksum_kernel(ChecksumArgs a) {
+    __shared__ uint32_t red[4][2];
+    const int u = blockIdx.x;
+    int s = 0;
+    while (s + 1 < a.n_seqs && a.unit_begin[s + 1] <= u) s++;
+    const int lu = u - a.unit_begin[s];
+    const int blk = lu >> 3, kv = (lu >> 2) & 1, hh = lu & 3;
+    const int L = a.kv_len[s];
+    const int32_t id = a.table[(size_t)a.slot[s] * a.table_stride + blk];
+    const uint16_t* unit = (kv ? a.vpool : a.kpool) + ((size_t)id * kKvHeads + hh) * (kBlockTok * kHeadDim);
+    const int t = threadIdx.x;
+    u32x4 w[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        w[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(unit) + j * 256 + t);
+    uint32_t lo = 0, hi = 0;
+    const int n_valid = min(kBlockTok, L - blk * kBlockTok);  // tokens of this block in the sequence
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int tok = j * 8 + (t >> 5);  // 32 x 16 B per token row
+        if (tok < n_valid) {
+            const uint32_t j0 = (uint32_t)(j * 256 + t) * 4;  // word index in the unit
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                lo += w[j][k];
+                hi += w[j][k] ^ (j0 + k);
+            }
+        }
+    }
+    lo = wave_sum_u32(lo);
+    hi = wave_sum_u32(hi);
+    if ((t & 63) == 0) {
+        red[t >> 6][0] = lo;
+        red[t >> 6][1] = hi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        uint2 r;
+        r.x = red[0][0] + red[1][0] + red[2][0] + red[3][0];
+        r.y = red[0][1] + red[1][1] + red[2][1] + red[3][1];
+        reinterpret_cast<uint2*>(a.out)[u] = r;
+    }
+}
+
 __global__ __launch_bounds__(256) void snapshot_kernel(SnapshotArgs a) {
     const int p = blockIdx.y;
     const int64_t u0 = snap_units_begin(a), u1 = snap_units_end(a);
@@ -2526,6 +2591,11 @@ int launch_decode(const DecodeArgs& a, void* stream) {
         hipLaunchKernelGGL(decode_kernel<2>, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
     else
         hipLaunchKernelGGL(decode_kernel<1>, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
+    return (int)hipGetLastError();
+}
+
+int launch_checksum(const ChecksumArgs& a, void* stream) {
+    hipLaunchKernelGGL(checksum_kernel, dim3((unsigned)a.n_units), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 

@@ -43,7 +43,7 @@ EXPORTS = [
     "kvc_get_stats", "kvc_abi_version", "kvc_seq_create", "kvc_seq_release",
     "kvc_seq_reset", "kvc_seq_len", "kvc_seq_truncate", "kvc_seq_reserve",
     "kvc_seq_commit", "kvc_prefix_match", "kvc_append", "kvc_qkv_append", "kvc_decode_attn",
-    "kvc_decode_attn_static", "kvc_prefill_attn", "kvc_gather", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
+    "kvc_decode_attn_static", "kvc_prefill_attn", "kvc_gather", "kvc_kv_checksum", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
     "kvc_snapshot_restore", "kvc_snapshot_release", "kvc_pool_fill_normal",
     "kvc_fill_normal_bf16", "kvc_sync",
 ]
@@ -114,6 +114,7 @@ def lib() -> ctypes.CDLL:
             "kvc_qkv_append": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, P, P]),
             "kvc_decode_attn": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
             "kvc_decode_attn_static": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
+            "kvc_kv_checksum": (ctypes.c_int, [P, I32, pI32, I32, P, P]),
             "kvc_prefill_attn": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P, I32, F32, P]),
             "kvc_gather": (ctypes.c_int, [P, I32, pI32, I32, I32, pI32, P, P, P]),
             "kvc_state_ptrs": (ctypes.c_int, [P, I32, I32, ctypes.POINTER(P), ctypes.POINTER(P)]),
@@ -394,6 +395,10 @@ class Context:
     def gather(self, layer, seqs, tok0, n_tok, k_out, v_out, stream=None):
         _check(self.L.kvc_gather(self.ptr, layer, _i32(seqs), len(seqs), tok0, _i32(n_tok),
                                  self._p(k_out), self._p(v_out), stream))
+
+    def kv_checksum(self, layer, seqs, out, stream=None):
+        """out (device uint64) = per-unit checksums of each seq's K/V in `layer`"""
+        _check(self.L.kvc_kv_checksum(self.ptr, layer, _i32(seqs), len(seqs), self._p(out), stream))
 
     def state_ptrs(self, s, ssm_layer):
         r, c = ctypes.c_void_p(), ctypes.c_void_p()

@@ -321,3 +321,25 @@ def finite_bf16_values() -> np.ndarray:
     b = np.arange(65536, dtype=np.uint32)
     f = (b << 16).view(np.float32)
     return f[np.isfinite(f)]
+
+
+def kv_checksums(k: np.ndarray, v: np.ndarray, n_kv: int = 4, d: int = 256, block: int = 32) -> np.ndarray:
+    """kvc_kv_checksum of one sequence and layer from its K and V in the
+    reference layout (bf16 bits [L][n_kv][d] each): one uint64 per (block,
+    K|V, kv head) unit in that order; over the unit's 32-bit words w_j of its
+    [token][d] rows (j = token * d/2 + word, tokens below L only), sum(w_j)
+    mod 2^32 in the low half and sum(w_j ^ j) mod 2^32 in the high half."""
+    L = k.shape[0]
+    nb = (L + block - 1) // block
+    out = np.zeros((nb, 2, n_kv), np.uint64)
+    for kv, x in enumerate((k, v)):
+        x = np.ascontiguousarray(x, np.uint16).reshape(L, n_kv, d)
+        for b in range(nb):
+            rows = x[b * block:(b + 1) * block]  # [tok][head][d], tokens < L only
+            for hh in range(n_kv):
+                w = np.ascontiguousarray(rows[:, hh, :]).view(np.uint32).ravel().astype(np.uint64)
+                j = np.arange(w.size, dtype=np.uint64)
+                lo = int(w.sum() & 0xFFFFFFFF)
+                hi = int((w ^ j).sum() & 0xFFFFFFFF)
+                out[b, kv, hh] = (hi << 32) | lo
+    return out.ravel()

@@ -5,7 +5,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 PKG = ROOT / "qwen3.5-9b-bfp8b-1xn300_amd"
-for p in (str(PKG), str(ROOT / "tests")):
+for p in (str(PKG), str(ROOT / "tests"), str(ROOT)):
     if p not in sys.path:
         sys.path.insert(0, p)
 

@@ -372,3 +372,47 @@ def test_attention_scale_sign_and_zero(scale):
             mk, mv = m.get(s, 0)
             ref = O.decode_attn(qd[i], mk, mv, prefixes[i] + n, scale=scale)
             O.assert_attn_close(outd[i], ref, what=f"decode L={prefixes[i] + n} scale={scale}")
+
+
+def test_kv_checksum_matches_host():
+    """kvc_kv_checksum over ragged sequences on a permuted pool equals the
+    per-unit checksums of the gathered reference-layout K/V in every layer;
+    a partial last block sums only the sequence's own keys, and one changed
+    key changes exactly the units that hold it."""
+    say("kv checksum vs host, ragged lengths")
+    h = kvc.hip()
+    with make_ctx() as ctx:
+        m = Mirror(LAYERS)
+        lens = [1, 31, 32, 45, 300]
+        seqs = [ctx.seq_create() for _ in lens]
+        for i, (s, L) in enumerate(zip(seqs, lens)):
+            fill_seq(ctx, m, [s], L, seed=6100 + i, chunk=64)
+        n_units = sum((L + 31) // 32 * 8 for L in lens)
+        out = h.malloc(8 * n_units)
+        for layer in range(LAYERS):
+            ctx.kv_checksum(layer, seqs, out)
+            ctx.sync()
+            got = out.download(np.uint64, (n_units,))
+            want = np.concatenate([O.kv_checksums(*m.get(s, layer)) for s in seqs])
+            assert np.array_equal(got, want), layer
+        # overwrite key 40 of sequence 3 (block 1) in layer 0: only its 4 K units change
+        s3 = seqs[3]
+        ctx.seq_truncate(s3, 40)
+        k_row = O.normal_bf16(ROW, 6200)
+        v_row = m.get(s3, 0)[1][40].copy()
+        ctx.reserve([s3], 1)
+        kb, vb = kvc.to_device(k_row), kvc.to_device(v_row)
+        ctx.append(0, [s3], 1, kb, vb)
+        ctx.commit([s3], 1)
+        kb.free()
+        vb.free()
+        mk, mv = m.get(s3, 0)
+        mk2 = np.concatenate([mk[:40], k_row.reshape(1, ROW)])
+        mv2 = mv[:41]
+        ctx.kv_checksum(0, [s3], out)
+        ctx.sync()
+        got = out.download(np.uint64, (16,))
+        assert np.array_equal(got, O.kv_checksums(mk2, mv2))
+        before = O.kv_checksums(mk[:41], mv[:41])
+        assert np.flatnonzero(got != before).tolist() == [8, 9, 10, 11]
+        out.free()

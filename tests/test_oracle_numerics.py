@@ -148,3 +148,31 @@ def test_schraudolph_exact_model_random_fp32():
     for x in xs[:2000].tolist():
         d = int(_bits(L.orc_fast_expf_rne(x))) - int(_bits(L.orc_fast_expf(x)))
         assert d in (0, 1), x
+
+
+def test_kv_checksum_definition():
+    """The host per-unit checksums on hand-made K/V: the plain word sum, and
+    the word sum with each word XORed with its index in the unit, both mod
+    2^32; moving one word changes only the second; keys past L count for
+    nothing."""
+    L = 33  # two blocks, the second holding one key
+    k = np.zeros((L, 4, 256), np.uint16)
+    v = np.zeros((L, 4, 256), np.uint16)
+    k[0, 0, 0] = 1            # K unit (block 0, head 0), word 0
+    v[32, 3, 255] = 0x8000    # V unit (block 1, head 3), word 127 of token 0: high half
+    c = O.kv_checksums(k, v)
+    assert c.shape == (2 * 2 * 4,)
+    tri = lambda n: n * (n - 1) // 2  # sum of j over j < n (0 ^ j = j)
+    full, one = 32 * 128, 1 * 128     # words of a full and of a one-key unit
+    assert c[0] == ((1 + tri(full) - 0) & 0xFFFFFFFF) << 32 | 1  # (1 ^ 0) + sum of the other j
+    assert c[1] == (tri(full) & 0xFFFFFFFF) << 32                 # an all-zero full unit
+    v_unit = 8 + 4 + 3                                            # block 1, V, head 3
+    want_hi = (tri(one) - 127 + (0x80000000 ^ 127)) & 0xFFFFFFFF
+    assert c[v_unit] == (want_hi << 32) | 0x80000000
+    k2 = k.copy()
+    k2[0, 0, 0], k2[0, 0, 2] = 0, 1  # the same word value, one word later
+    c2 = O.kv_checksums(k2, v)
+    assert (c2[0] & 0xFFFFFFFF) == (c[0] & 0xFFFFFFFF) and c2[0] != c[0]
+    assert np.array_equal(c2[1:], c[1:])
+    k3 = np.concatenate([k, np.full((1, 4, 256), 7, np.uint16)])[:L]  # nothing past L is read
+    assert np.array_equal(O.kv_checksums(k3, v), c)
