@@ -47,12 +47,13 @@ DN_TOKEN_FLOP = 32 * 128 * 128 * 7  # delta rule, one token and layer: 7 flop pe
 METRIC = "KV path HBM GB/s (% of 8 TB/s) + µs/layer decode attn at 4K ctx, 1 GPU"
 
 
-def profiled_traffic(name: str):
-    """HBM bytes per launch recorded by a committed rocprofv3 PMC summary."""
+def profiled_traffic(name: str, key: str = "traffic_bytes_per_launch"):
+    """HBM bytes per launch recorded by a committed rocprofv3 PMC summary
+    (the `key: value` line of profiles/<name>)."""
     try:
         for ln in (ROOT / "profiles" / name).read_text().splitlines():
-            if ln.strip().startswith("traffic_bytes_per_launch"):
-                return int(float(ln.split(":", 1)[1]))
+            if ln.strip().startswith(key + " ") or ln.strip().startswith(key + ":"):
+                return int(float(ln.split(":", 1)[1].replace(",", "")))
     except (OSError, ValueError):
         pass
     return None
@@ -62,12 +63,20 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def host_cores() -> int:
+# The GPU box's CPU share for one GPU is 16 threads (its OMP_NUM_THREADS);
+# the CPU baselines use at most that many, and report the affinity count.
+CORE_CAP = 16
+
+
+def affinity_cores() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        return os.cpu_count() or 1
+
+
+def host_cores() -> int:
+    return max(1, min(affinity_cores(), CORE_CAP))
 
 
 def cpu_model() -> str:
@@ -538,6 +547,16 @@ def run_d(args):
 # ---------------------------------------------------------------------------
 # config c: multi-turn prefix reuse, 64 sessions, 128-token chunked prefill
 
+def hbm_rate(leg: str, us: float, key: str):
+    """Counter-measured HBM GB/s of a config-c leg from the committed profile."""
+    t = profiled_traffic("prefill_gather_c.txt", key)
+    if t is None:
+        return {}
+    gbs = t / (us * 1e-6) / 1e9
+    return {f"{leg}_hbm_bytes_per_launch": t, f"{leg}_hbm_GBps": round(gbs, 1),
+            f"{leg}_hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1)}
+
+
 def run_c(args):
     import kvc
 
@@ -635,9 +654,13 @@ def run_c(args):
             "qkv_append_us_per_layer": round(qa_us, 1),
             "qkv_append_GBps": round(qa_bytes / (qa_us * 1e-6) / 1e9, 1),
             "gather_us_per_layer": round(g_us, 1), "gather_GBps": round(g_bytes / (g_us * 1e-6) / 1e9, 1),
+            # HBM bytes actually moved (rocprofv3 counters): the 64 sessions share
+            # 8 base prefixes, so part of the algorithmic reads hit in cache
+            **hbm_rate("gather", g_us, "gather_traffic_bytes_per_launch"),
             "prefill_us_per_layer": round(p_us, 1),
             "prefill_TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 2),
             "prefill_GBps": round(p_bytes / (p_us * 1e-6) / 1e9, 1),
+            **hbm_rate("prefill", p_us, "prefill_traffic_bytes_per_launch"),
             "mean_prefix": float(P.mean()),
             **({} if args.no_cpu else {"cpu_baseline": cpu_baseline_c(P)})}
 
@@ -826,6 +849,11 @@ def main():
             others[name] = runners[name](args)
     if others:
         line["configs"] = others
+    if "cpu_baseline" in line:
+        line["cpu_baseline"]["affinity_cores"] = affinity_cores()
+        line["cpu_baseline"]["core_cap"] = CORE_CAP
+        line["cpu_baseline"]["core_note"] = (f"threads capped at {CORE_CAP}, the host's CPU share for one GPU; "
+                                             f"{affinity_cores()} cores in this process's affinity mask")
     print(json.dumps(line), flush=True)
 
 
