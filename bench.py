@@ -39,6 +39,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "qwen3.5-9b-bfp8b-1xn300_amd"))
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 NQ, NKV, D, BT = 16, 4, 256, 32
 ROW = NKV * D
 SEED = 20261201
@@ -547,6 +548,38 @@ def run_d(args):
 # ---------------------------------------------------------------------------
 # config c: multi-turn prefix reuse, 64 sessions, 128-token chunked prefill
 
+def mfma_data_ceiling():
+    """The dense bf16 MFMA rate the prefill's operand data allows, measured
+    on this GPU with libkvc_calib.so: an MFMA-only v_mfma_f32_32x32x16_bf16
+    loop at 4 waves per SIMD with constant operands, with N(0,1) x N(0,1)
+    operands (the S = K Q^T half of the prefill's flops) and with N(0,1) x
+    U[0,1) operands (the O += V^T P^T half).  The prefill ceiling is the
+    time-weighted (harmonic) mean of the last two."""
+    import ctypes
+
+    path = ROOT / "qwen3.5-9b-bfp8b-1xn300_amd" / "libkvc_calib.so"
+    if not path.exists():
+        return {}
+    lib = ctypes.CDLL(str(path))
+    lib.kvc_calib_mfma_bf16.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    rate = {}
+    for name, mode in (("const", 0), ("normal_x_normal", 1), ("normal_x_unit", 2)):
+        out = ctypes.c_double(0.0)
+        rc = lib.kvc_calib_mfma_bf16(mode, 256, 20, ctypes.byref(out))
+        if rc != 0:
+            return {}
+        rate[name] = round(out.value, 1)
+    ceiling = 2.0 / (1.0 / rate["normal_x_normal"] + 1.0 / rate["normal_x_unit"])
+    return {"mfma_rate_TFLOPs": rate, "mfma_data_ceiling_TFLOPs": round(ceiling, 1)}
+
+
+def ceiling_fields(tflops: float):
+    c = mfma_data_ceiling()
+    if not c:
+        return {}
+    return {**c, "prefill_pct_of_data_ceiling": round(100 * tflops / c["mfma_data_ceiling_TFLOPs"], 1)}
+
+
 def hbm_rate(leg: str, us: float, key: str):
     """Counter-measured HBM GB/s of a config-c leg from the committed profile."""
     t = profiled_traffic("prefill_gather_c.txt", key)
@@ -659,6 +692,8 @@ def run_c(args):
             **hbm_rate("gather", g_us, "gather_traffic_bytes_per_launch"),
             "prefill_us_per_layer": round(p_us, 1),
             "prefill_TFLOPs": round(flops / (p_us * 1e-6) / 1e12, 2),
+            "prefill_pct_of_bf16_peak": round(100 * flops / (p_us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 1),
+            **ceiling_fields(flops / (p_us * 1e-6) / 1e12),
             "prefill_GBps": round(p_bytes / (p_us * 1e-6) / 1e9, 1),
             **hbm_rate("prefill", p_us, "prefill_traffic_bytes_per_launch"),
             "mean_prefix": float(P.mean()),

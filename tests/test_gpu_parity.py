@@ -319,6 +319,48 @@ def test_prefill_long_prefix_gate_bf16():
             O.assert_attn_close(out[i], ref, rel_rms=5e-3, what=f"prefill P={P} tight")
 
 
+@pytest.mark.parametrize("a,b", [(2.0, 1.0), (4.0, 4.0)])
+def test_prefill_scores_far_above_first_tile(a, b):
+    """The prefill kernel's exponent offset is each row's score maximum over
+    the first 64 keys.  One key of a later tile is made to score far above it:
+    q = a everywhere and key 150 = b everywhere, so that key scores 16 a b
+    (46 above in the log2 domain for (2, 1): large weights, no overflow) while
+    the first tile's keys score ~N(0, a^2).  (4, 4) overflows the weights
+    (~360 above), so the wave's outputs are not finite and it recomputes its
+    rows with the exact fallback.  Both must match the oracle, which
+    subtracts the true maximum."""
+    say(f"prefill, one key far above the first tile (a={a}, b={b})")
+    P, n, hot = 300, 64, 150
+    with make_ctx() as ctx:
+        h = kvc.hip()
+        s = ctx.seq_create()
+        k = O.normal_bf16((P + n) * ROW, 9301).reshape(P + n, ROW)
+        v = O.normal_bf16((P + n) * ROW, 9302).reshape(P + n, ROW)
+        k[hot] = O.f32_to_bf16(np.full(ROW, b, np.float32))
+        q = O.f32_to_bf16(np.full(n * NQ * D, a, np.float32)).reshape(n, NQ, D)
+        ctx.reserve([s], P)
+        kb, vb = h.malloc(k.nbytes).upload(k[:P]), h.malloc(v.nbytes).upload(v[:P])
+        ctx.append(0, [s], P, kb, vb)
+        ctx.commit([s], P)
+        ctx.reserve([s], n)
+        kb.upload(k[P:])
+        vb.upload(v[P:])
+        ctx.append(0, [s], n, kb, vb)
+        qb = h.malloc(q.nbytes).upload(q)
+        ob = h.malloc(n * NQ * D * 4)
+        ctx.prefill_attn(0, [s], n, qb, ob)
+        ctx.sync()
+        out = ob.download(np.float32, (n, NQ, D))
+        for b_ in (kb, vb, qb, ob):
+            b_.free()
+        assert np.isfinite(out).all()
+        ref = O.prefill_attn(q, k, v, P, n)
+        O.assert_attn_close(out, ref, what=f"prefill far scores a={a} b={b}")
+        O.assert_attn_close(out, ref, rel_rms=3e-3, what="tight")
+        # every row sees key 150: its V row dominates (weight ~1 - 2^-39 or more)
+        np.testing.assert_allclose(out[:, 0, :], np.broadcast_to(O.bf16_to_f32(v[hot, :D]), (n, D)), atol=1e-3)
+
+
 @pytest.mark.parametrize("scale", [-1.0 / 16, 0.0, 1.0 / 8])
 def test_attention_scale_sign_and_zero(scale):
     """Decode and prefill take any finite softmax scale.  The prefill kernel
