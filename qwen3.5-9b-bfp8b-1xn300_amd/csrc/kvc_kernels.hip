@@ -1168,26 +1168,39 @@ void prefill_mfma_kernel(PrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Append: one workgroup per (sequence, token) moves that token's K and V rows
-// (4 heads x 512 B each); thread t copies 16 B: kv = t / 128, head =
-// (t / 32) % 4, piece = t % 32.  The sequence, position and block id are
+// Append: one workgroup per (sequence, 4 consecutive tokens) moves those
+// tokens' K and V rows (4 heads x 512 B each); thread t copies one 16-B piece
+// of every token: kv = t / 128, head = (t / 32) % 4, piece = t % 32.  All of a
+// thread's loads are issued before its stores.  The sequence and positions are
 // workgroup-uniform (scalar), so no lane does index division.  The pool store
-// is non-temporal (streamed past L2): measured 11.9 us for 64 x 128 tokens
-// against 14.9 us with a plain store; more tokens per workgroup gained no more.
+// is non-temporal (streamed past L2): for 64 x 128 tokens, 1 token per
+// workgroup ran 11.9 us with non-temporal stores (14.9 us with plain ones) and
+// 4 tokens per workgroup run 9.8 us.
+constexpr int kAppendTok = 4;  // tokens per append workgroup
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
-    const int b = blockIdx.x;
-    const int s = b / a.n_tok;
-    const int tok = b - s * a.n_tok;
-    const int pos = a.pos0[s] + tok;
-    const int blk = a.table[(size_t)a.slot[s] * a.table_stride + pos / kBlockTok];
+    const int per_seq = (a.n_tok + kAppendTok - 1) / kAppendTok;
+    const int s = blockIdx.x / per_seq;
+    const int tok0 = (blockIdx.x - s * per_seq) * kAppendTok;
     const int t = threadIdx.x;
     const int kv = t >> 7, h = (t >> 5) & 3, part = t & 31;
-    const size_t dst = (((size_t)blk * kKvHeads + h) * kBlockTok + pos % kBlockTok) * kHeadDim + part * 8;
-    const size_t src = (((size_t)s * a.n_tok + tok) * kKvHeads + h) * kHeadDim + part * 8;
     const uint16_t* from = kv ? a.v : a.k;
     uint16_t* to = kv ? a.vpool : a.kpool;
-    const u32x4 x = *reinterpret_cast<const u32x4*>(from + src);
-    __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(to + dst));
+    const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
+    u32x4 x[kAppendTok];
+#pragma unroll
+    for (int i = 0; i < kAppendTok; i++) {
+        const int tok = min(tok0 + i, a.n_tok - 1);
+        const size_t src = (((size_t)s * a.n_tok + tok) * kKvHeads + h) * kHeadDim + part * 8;
+        x[i] = *reinterpret_cast<const u32x4*>(from + src);
+    }
+#pragma unroll
+    for (int i = 0; i < kAppendTok; i++) {
+        if (tok0 + i >= a.n_tok) break;
+        const int pos = a.pos0[s] + tok0 + i;
+        const int blk = trow[pos / kBlockTok];
+        const size_t dst = (((size_t)blk * kKvHeads + h) * kBlockTok + pos % kBlockTok) * kHeadDim + part * 8;
+        __builtin_nontemporal_store(x[i], reinterpret_cast<u32x4*>(to + dst));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1203,15 +1216,15 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 // rope_dim >= 16, the other half of the lane's own 8 dims for rope_dim = 8.
 // Arithmetic follows the reference's order (src/engine.cpp:3497-3512,
 // :2422-2432): (x * r) * w, then x0 c - x1 s and x1 c + x0 s without
-// contraction.  Projection rows are read once and every output written once:
-// both go non-temporal.
+// contraction.  Every output is written once and goes non-temporal; the
+// projection rows are read with plain loads (64 x 128 tokens of bf16 input:
+// 57.7 us, against 61.0 us with non-temporal loads).
 constexpr int kQkvWaves = 5;
 
 template <bool BF16IN>
 __device__ __forceinline__ void load_row8(const void* base, size_t off, float (&x)[8]) {
     if constexpr (BF16IN) {
-        const u32x4 u =
-            __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off));
+        const u32x4 u = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             x[2 * j] = bf16lo(u[j]);
@@ -1219,8 +1232,8 @@ __device__ __forceinline__ void load_row8(const void* base, size_t off, float (&
         }
     } else {
         const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + off);
-        const u32x4 f0 = __builtin_nontemporal_load(src);
-        const u32x4 f1 = __builtin_nontemporal_load(src + 1);
+        const u32x4 f0 = src[0];
+        const u32x4 f1 = src[1];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             x[j] = __uint_as_float(f0[j]);
@@ -1253,66 +1266,71 @@ __device__ __forceinline__ float half_wave_sum(float x) {
     return sum_xor16(x);
 }
 
+// tokens per producer workgroup (all their rows are loaded first); 2 and 4
+// tokens measured no faster than 1
+constexpr int kQkvTok = 1;
 template <bool BF16IN>
 __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
 #pragma clang fp contract(off)
-    const int b = blockIdx.x;
-    const int s = b / a.n_tok;
-    const int tok = b - s * a.n_tok;
-    const int pos = a.pos0[s] + tok;
+    const int per_seq = (a.n_tok + kQkvTok - 1) / kQkvTok;
+    const int s = blockIdx.x / per_seq;
+    const int tok0 = (blockIdx.x - s * per_seq) * kQkvTok;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int hl = lane & 31, sub = lane >> 5;  // lane in the half, which half
     const int d0 = hl * 8;
-    const size_t row = ((size_t)s * a.n_tok + tok) * kQkvRow;
-    const size_t orow = ((size_t)s * a.n_tok + tok) * kQHeads * kHeadDim;
     const bool kv_wave = wave == kQkvWaves - 1;  // rows 16..19: the kv heads
     constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
-
-    // every input row of this lane is requested before anything is stored:
-    // rows 4w + 2i + sub of [q 0..15, k 0..3] (normalized) and of
-    // [gate 0..15, v 0..3] (copied)
-    // copied rows of bf16 input go through as raw 16-B pieces (RNE of a bf16
-    // value is itself); fp32 input is converted
-    float x[2][8], c[2][8];
-    u32x4 craw[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int r = wave * 4 + i * 2 + sub;
-        const size_t xo = kv_wave ? row + kKOff + (size_t)(r - kQHeads) * kHeadDim : row + (size_t)r * 2 * kHeadDim;
-        const size_t co = kv_wave ? row + kKOff + (size_t)(kKvHeads + r - kQHeads) * kHeadDim
-                                  : row + (size_t)r * 2 * kHeadDim + kHeadDim;
-        load_row8<BF16IN>(a.qkv, xo + d0, x[i]);
-        if (kv_wave || a.gate_out) {
-            if constexpr (BF16IN)
-                craw[i] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qkv) + co + d0));
-            else
-                load_row8<BF16IN>(a.qkv, co + d0, c[i]);
-        }
-    }
-    const int blk = a.table[(size_t)a.slot[s] * a.table_stride + pos / kBlockTok];
-    // RoPE coefficients of this lane's 8 dims: table entries p0 .. p0+7 for
-    // rope_dim >= 16, entries 0..3 twice for rope_dim 8
     const int half = a.rope_half;
     const bool roped = d0 < 2 * half;
-    float cs[8], sn[8];
-    if (roped) {
-        const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
-        const float* crow = a.rope + (size_t)pos * half + p0;
-        const float* srow = a.rope + ((size_t)a.rope_rows + pos) * half + p0;
-        const float4 c0 = *reinterpret_cast<const float4*>(crow);
-        const float4 s0 = *reinterpret_cast<const float4*>(srow);
-        const float4 c1 = half >= 8 ? *reinterpret_cast<const float4*>(crow + 4) : c0;
-        const float4 s1 = half >= 8 ? *reinterpret_cast<const float4*>(srow + 4) : s0;
-        cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w;
-        cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
-        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
-        sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
-    } else {
+    const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
+
+    // every input row of this lane, for every token of the workgroup, is
+    // requested before anything is stored: rows 4w + 2i + sub of [q 0..15,
+    // k 0..3] (normalized) and of [gate 0..15, v 0..3] (copied); copied rows
+    // of bf16 input go through as raw 16-B pieces (RNE of a bf16 value is
+    // itself), fp32 input is converted
+    float x[kQkvTok][2][8], c[kQkvTok][2][8];
+    u32x4 craw[kQkvTok][2];
+    float cs[kQkvTok][8], sn[kQkvTok][8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            cs[j] = 1.f;
-            sn[j] = 0.f;
+    for (int tt = 0; tt < kQkvTok; tt++) {
+        const int tok = min(tok0 + tt, a.n_tok - 1);
+        const size_t row = ((size_t)s * a.n_tok + tok) * kQkvRow;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int r = wave * 4 + i * 2 + sub;
+            const size_t xo = kv_wave ? row + kKOff + (size_t)(r - kQHeads) * kHeadDim : row + (size_t)r * 2 * kHeadDim;
+            const size_t co = kv_wave ? row + kKOff + (size_t)(kKvHeads + r - kQHeads) * kHeadDim
+                                      : row + (size_t)r * 2 * kHeadDim + kHeadDim;
+            load_row8<BF16IN>(a.qkv, xo + d0, x[tt][i]);
+            if (kv_wave || a.gate_out) {
+                if constexpr (BF16IN)
+                    craw[tt][i] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qkv) + co + d0);
+                else
+                    load_row8<BF16IN>(a.qkv, co + d0, c[tt][i]);
+            }
+        }
+        // RoPE coefficients of this lane's 8 dims: table entries p0 .. p0+7
+        // for rope_dim >= 16, entries 0..3 twice for rope_dim 8
+        const int pos = a.pos0[s] + tok;
+        if (roped) {
+            const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
+            const float* crow = a.rope + (size_t)pos * half + p0;
+            const float* srow = a.rope + ((size_t)a.rope_rows + pos) * half + p0;
+            const float4 c0 = *reinterpret_cast<const float4*>(crow);
+            const float4 s0 = *reinterpret_cast<const float4*>(srow);
+            const float4 c1 = half >= 8 ? *reinterpret_cast<const float4*>(crow + 4) : c0;
+            const float4 s1 = half >= 8 ? *reinterpret_cast<const float4*>(srow + 4) : s0;
+            cs[tt][0] = c0.x; cs[tt][1] = c0.y; cs[tt][2] = c0.z; cs[tt][3] = c0.w;
+            cs[tt][4] = c1.x; cs[tt][5] = c1.y; cs[tt][6] = c1.z; cs[tt][7] = c1.w;
+            sn[tt][0] = s0.x; sn[tt][1] = s0.y; sn[tt][2] = s0.z; sn[tt][3] = s0.w;
+            sn[tt][4] = s1.x; sn[tt][5] = s1.y; sn[tt][6] = s1.z; sn[tt][7] = s1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                cs[tt][j] = 1.f;
+                sn[tt][j] = 0.f;
+            }
         }
     }
     const float* wrow = (kv_wave ? a.k_norm : a.q_norm) + d0;
@@ -1320,67 +1338,76 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
     const float4 w1 = *reinterpret_cast<const float4*>(wrow + 4);
     const float wn[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 
-    // copied rows: gate heads, or (wave 4) the v heads
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int r = wave * 4 + i * 2 + sub;
-        if (kv_wave) {
-            const size_t slot =
-                (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
-            if constexpr (BF16IN)
-                __builtin_nontemporal_store(craw[i], reinterpret_cast<u32x4*>(a.vpool + slot));
-            else
-                store_bf16x8(a.vpool + slot, c[i]);
-        } else if (a.gate_out) {
-            if constexpr (BF16IN)
-                __builtin_nontemporal_store(craw[i], reinterpret_cast<u32x4*>(a.gate_out + orow + (size_t)r * kHeadDim + d0));
-            else
-                store_bf16x8(a.gate_out + orow + (size_t)r * kHeadDim + d0, c[i]);
+    for (int tt = 0; tt < kQkvTok; tt++) {
+        if (tok0 + tt >= a.n_tok) break;  // uniform
+        const int tok = tok0 + tt;
+        const int pos = a.pos0[s] + tok;
+        const size_t orow = ((size_t)s * a.n_tok + tok) * kQHeads * kHeadDim;
+        const int blk = trow[pos / kBlockTok];
+        // copied rows: gate heads, or (wave 4) the v heads
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int r = wave * 4 + i * 2 + sub;
+            if (kv_wave) {
+                const size_t slot =
+                    (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
+                if constexpr (BF16IN)
+                    __builtin_nontemporal_store(craw[tt][i], reinterpret_cast<u32x4*>(a.vpool + slot));
+                else
+                    store_bf16x8(a.vpool + slot, c[tt][i]);
+            } else if (a.gate_out) {
+                if constexpr (BF16IN)
+                    __builtin_nontemporal_store(craw[tt][i],
+                                                reinterpret_cast<u32x4*>(a.gate_out + orow + (size_t)r * kHeadDim + d0));
+                else
+                    store_bf16x8(a.gate_out + orow + (size_t)r * kHeadDim + d0, c[tt][i]);
+            }
         }
-    }
-    // normalized rows: RMSNorm, RoPE, bf16
+        // normalized rows: RMSNorm, RoPE, bf16
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int r = wave * 4 + i * 2 + sub;  // 0..15 q heads, 16..19 k heads
-        float ss = 0.f;
+        for (int i = 0; i < 2; i++) {
+            const int r = wave * 4 + i * 2 + sub;  // 0..15 q heads, 16..19 k heads
+            float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) ss += x[i][j] * x[i][j];
-        ss = half_wave_sum(ss);
-        const float rs = 1.0f / sqrtf(ss / kHeadDim + a.eps);
-        float y[8];
+            for (int j = 0; j < 8; j++) ss += x[tt][i][j] * x[tt][i][j];
+            ss = half_wave_sum(ss);
+            const float rs = 1.0f / sqrtf(ss / kHeadDim + a.eps);
+            float y[8];
 #pragma unroll
-        for (int j = 0; j < 8; j++) y[j] = x[i][j] * rs * wn[j];
-        if (half >= 8) {
-            float yp[8];
-            switch (half) {  // partner lane ^ (half / 8), uniform
-                case 8: swap_lanes8<1>(y, yp); break;
-                case 16: swap_lanes8<2>(y, yp); break;
-                case 32: swap_lanes8<4>(y, yp); break;
-                case 64: swap_lanes8<8>(y, yp); break;
-                default: swap_lanes8<16>(y, yp); break;
+            for (int j = 0; j < 8; j++) y[j] = x[tt][i][j] * rs * wn[j];
+            if (half >= 8) {
+                float yp[8];
+                switch (half) {  // partner lane ^ (half / 8), uniform
+                    case 8: swap_lanes8<1>(y, yp); break;
+                    case 16: swap_lanes8<2>(y, yp); break;
+                    case 32: swap_lanes8<4>(y, yp); break;
+                    case 64: swap_lanes8<8>(y, yp); break;
+                    default: swap_lanes8<16>(y, yp); break;
+                }
+                if (roped) {
+                    const bool low = d0 < half;
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        y[j] = low ? y[j] * cs[tt][j] - yp[j] * sn[tt][j] : y[j] * cs[tt][j] + yp[j] * sn[tt][j];
+                }
+            } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
+                float z[8];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    z[j] = y[j] * cs[tt][j] - y[j + 4] * sn[tt][j];
+                    z[j + 4] = y[j + 4] * cs[tt][j + 4] + y[j] * sn[tt][j + 4];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = z[j];
             }
-            if (roped) {
-                const bool low = d0 < half;
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    y[j] = low ? y[j] * cs[j] - yp[j] * sn[j] : y[j] * cs[j] + yp[j] * sn[j];
+            if (kv_wave) {
+                const size_t slot =
+                    (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
+                store_bf16x8(a.kpool + slot, y);
+            } else if (a.q_out) {
+                store_bf16x8(a.q_out + orow + (size_t)r * kHeadDim + d0, y);
             }
-        } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
-            float z[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                z[j] = y[j] * cs[j] - y[j + 4] * sn[j];
-                z[j + 4] = y[j + 4] * cs[j + 4] + y[j] * sn[j + 4];
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) y[j] = z[j];
-        }
-        if (kv_wave) {
-            const size_t slot =
-                (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
-            store_bf16x8(a.kpool + slot, y);
-        } else if (a.q_out) {
-            store_bf16x8(a.q_out + orow + (size_t)r * kHeadDim + d0, y);
         }
     }
 }
@@ -2337,21 +2364,25 @@ __global__ __launch_bounds__(256) void zero_state_kernel(ZeroStateArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Gather: work item = (sequence, 32 consecutive output tokens), split over 8
-// workgroups = (K or V) x (8-token quarter); output rows are [tok][kv_head][d]
-// packed back to back.  A workgroup moves 16 KiB: each thread 4 x 16 B, all
-// loads issued before the stores.  The quarter's at most two block ids are
-// read once per workgroup (scalar loads), so no table load precedes a data
-// load.
+// Gather: work item = (sequence, 32 consecutive output tokens), split over 4
+// workgroups = (K or V) x (16-token half); output rows are [tok][kv_head][d]
+// packed back to back.  A workgroup moves 32 KiB: each thread 8 x 16 B, all
+// loads issued before the stores.  The half's at most two block ids are read
+// once per workgroup (scalar loads), so no table load precedes a data load.
+// Pool reads are plain loads, output stores non-temporal: for config c's
+// 16 x 8192 tokens x 8 layers, 8-token quarters with non-temporal loads ran
+// 157 us, 16-token halves with plain loads run 127 us.
+constexpr int kGatherQ = 2;                          // workgroups per 32-token chunk and K|V
+constexpr int kGatherTok = kBlockTok / kGatherQ;     // tokens per workgroup
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
-    const int item = blockIdx.x >> 3;
-    const int kv = (blockIdx.x >> 2) & 1, q8 = blockIdx.x & 3;
+    const int item = blockIdx.x / (2 * kGatherQ);
+    const int kv = (blockIdx.x / kGatherQ) & 1, q8 = blockIdx.x % kGatherQ;
     int s = 0;
     while (s + 1 < a.n_seqs && a.item_begin[s + 1] <= item) s++;
     const int c = item - a.item_begin[s];
     const int n_tok = a.out_begin[s + 1] - a.out_begin[s];
-    const int t0 = c * kBlockTok + q8 * 8;
-    const int nt = min(8, n_tok - t0);
+    const int t0 = c * kBlockTok + q8 * kGatherTok;
+    const int nt = min(kGatherTok, n_tok - t0);
     if (nt <= 0) return;
     const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
     const int p0 = a.tok0 + t0;
@@ -2360,7 +2391,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
     const uint16_t* __restrict__ pool = kv ? a.vpool : a.kpool;
     uint16_t* __restrict__ outp = (kv ? a.v_out : a.k_out) + ((size_t)a.out_begin[s] + t0) * kKvHeads * kHeadDim;
     constexpr int kRowUnits = kHeadDim * 2 / 16;  // 32 x 16 B per (token, head) row
-    constexpr int kPer = 8 * kKvHeads * kRowUnits / 256;  // 4
+    constexpr int kPer = kGatherTok * kKvHeads * kRowUnits / 256;  // 16-B pieces per thread
     u32x4 buf[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
@@ -2371,7 +2402,7 @@ __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
         const int pos = p0 + min(tok, nt - 1);
         const int id = pos / kBlockTok == blk_a ? id_a : id_b;
         const size_t src = (((size_t)id * kKvHeads + hh) * kBlockTok + pos % kBlockTok) * kHeadDim + part * 8;
-        buf[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pool + src));
+        buf[j] = *reinterpret_cast<const u32x4*>(pool + src);
     }
 #pragma unroll
     for (int j = 0; j < kPer; j++) {
@@ -2606,14 +2637,15 @@ int launch_prefill(const PrefillArgs& a, void* stream) {
 }
 
 int launch_append(const AppendArgs& a, void* stream) {
-    static_assert(2 * kKvHeads * kHeadDim * 2 / 16 == 256, "one 16-B piece per thread of a 256-thread workgroup");
-    hipLaunchKernelGGL(append_kernel, dim3(a.n_seqs * a.n_tok), dim3(256), 0, (hipStream_t)stream, a);
+    static_assert(2 * kKvHeads * kHeadDim * 2 / 16 == 256, "one 16-B piece of each token per thread of a 256-thread workgroup");
+    hipLaunchKernelGGL(append_kernel, dim3(a.n_seqs * ((a.n_tok + kAppendTok - 1) / kAppendTok)), dim3(256), 0,
+                       (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
 int launch_qkv_append(const QkvArgs& a, void* stream) {
     static_assert(kQkvWaves * 4 == kQHeads + kKvHeads, "two pairs of head rows per wave");
-    const dim3 grid(a.n_seqs * a.n_tok), block(kQkvWaves * 64);
+    const dim3 grid(a.n_seqs * ((a.n_tok + kQkvTok - 1) / kQkvTok)), block(kQkvWaves * 64);
     if (a.in_bf16)
         hipLaunchKernelGGL(qkv_append_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
     else
@@ -2675,7 +2707,7 @@ int launch_zero_state(const ZeroStateArgs& a, void* stream) {
 
 int launch_gather(const GatherArgs& a, void* stream) {
     if (a.n_items <= 0) return 0;
-    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)a.n_items * 8), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)a.n_items * 2 * kGatherQ), dim3(256), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
