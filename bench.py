@@ -94,8 +94,8 @@ def cpu_model() -> str:
 # config b: single-sequence decode at 4K
 
 def bytes_per_layer_b(L=4096):
-    # K/V of L tokens + q + out (bf16) + append read/write of one token
-    return L * ROW * 2 * 2 + NQ * D * 2 + NQ * D * 2 + 2 * ROW * 2 * 2
+    # K/V of L tokens + q + gate + out (bf16) + append read/write of one token
+    return L * ROW * 2 * 2 + 3 * NQ * D * 2 + 2 * ROW * 2 * 2
 
 
 def cpu_baseline_b(L=4096, budget_s=12.0):
@@ -125,8 +125,9 @@ def cpu_baseline_b(L=4096, budget_s=12.0):
 
 class DecodeB:
     """Config b exactly as benched: one sequence per cache replica at L - 1
-    tokens, 8 layers, fused 1-token append + decode per layer (automatic
-    chunk and output-dim split), bf16 output.  One HIP graph holds a round of
+    tokens, 8 layers, fused 1-token append + gated decode per layer (the
+    reference's sigma(gate) * attention, automatic chunk and output-dim
+    split), bf16 output.  One HIP graph holds a round of
     `reps` steps (step r decodes replica r; kernel arguments carry each
     sequence's length); one graph per replica serves the steps left over when
     K is not a multiple of reps.  Per round the host reserves the appended
@@ -157,10 +158,12 @@ class DecodeB:
         self.kn = h.malloc(n * ROW * 2)
         self.vn = h.malloc(n * ROW * 2)
         self.out = h.malloc(n * NQ * D * 2)
+        self.gate = h.malloc(n * NQ * D * 2)
         self.sums = h.malloc(8 * n * (L // BT) * 2 * NKV)  # per-unit checksums of each (replica, layer)
         ctx.fill_normal_bf16(self.q, n * NQ * D, SEED + 4, 1.0, stream)
         ctx.fill_normal_bf16(self.kn, n * ROW, SEED + 5, 1.0, stream)
         ctx.fill_normal_bf16(self.vn, n * ROW, SEED + 6, 1.0, stream)
+        ctx.fill_normal_bf16(self.gate, n * NQ * D, SEED + 7, 1.0, stream)
         h.stream_sync(stream)
         ctx.reserve(seqs, 1, stream)
         self.graph = h.capture(stream, lambda: [self.enqueue_step(r) for r in range(reps)])
@@ -177,7 +180,8 @@ class DecodeB:
             i = r * self.layers + layer
             self.ctx.decode_attn(layer, [self.seqs[r]], self.q.ptr + i * NQ * D * 2, self.out.ptr + i * NQ * D * 2,
                                  k_new=self.kn.ptr + i * ROW * 2, v_new=self.vn.ptr + i * ROW * 2,
-                                 out_dtype=self.kvc.DTYPE_BF16, scale=1.0 / 16, stream=self.stream)
+                                 gate=self.gate.ptr + i * NQ * D * 2, out_dtype=self.kvc.DTYPE_BF16,
+                                 scale=1.0 / 16, stream=self.stream)
 
     def enqueue_floor(self, r):
         per = (self.L // BT) * 2 * NKV
@@ -216,7 +220,7 @@ class DecodeB:
     def close(self):
         for g_ in [self.graph, self.floor_graph] + self.single:
             self.h.graph_destroy(g_)
-        for b_ in (self.q, self.kn, self.vn, self.out, self.sums):
+        for b_ in (self.q, self.kn, self.vn, self.out, self.gate, self.sums):
             b_.free()
         self.ctx.close()
 
@@ -271,8 +275,8 @@ def run_b(args):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "b: single-sequence decode step, 8 full-attention layers, 16q/4kv heads, "
-                               "head_dim 256, bf16 cache at 4096 tokens, fused 1-token append + GQA decode "
-                               "per layer, HIP-graph replay, 4 rotated cache replicas (512 MiB)",
+                               "head_dim 256, bf16 cache at 4096 tokens, fused 1-token append + gated GQA "
+                               "decode per layer, HIP-graph replay, 4 rotated cache replicas (512 MiB)",
                    "layers": layers, "ctx": L, "replicas": reps},
         "us_per_layer": round(us_layer, 3),
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
@@ -295,7 +299,8 @@ def run_b(args):
         line["cpu_baseline"] = {
             "value": round(bpl / (usN * 1e-6) / 1e9, 2), "unit": "GB/s", "cores": cores, "kind": "port",
             "us_per_layer": round(usN, 1),
-            "sample": f"oracle decode over 4096 keys, 16 q heads, {nN} layer-decodes on {cores} threads "
+            "sample": f"oracle decode over 4096 keys, 16 q heads (no gate multiply: 4096 sigmoids, "
+                      f"under 0.02% of the work), {nN} layer-decodes on {cores} threads "
                       f"({cpu_model()})",
             "single_thread": {"value": round(bpl / (us1 * 1e-6) / 1e9, 2), "unit": "GB/s",
                               "us_per_layer": round(us1, 1), "layer_decodes": n1},

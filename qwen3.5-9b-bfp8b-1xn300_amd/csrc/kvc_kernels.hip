@@ -328,13 +328,13 @@ __device__ __forceinline__ float gate_sigmoid(float x, int ref) {
     return ref ? sigmoid_ref(x) : sigmoidf_exact(x);
 }
 
-// out row = A / L (* sigmoid(gate)), written as bf16 (RNE) or fp32.
-__device__ __forceinline__ void write_out(void* out, int out_bf16, size_t row_off, int d0,
-                                          const uint16_t* gate_row, int gate_ref, float L, const float (&A)[4]) {
+// out row = A / L (* sigmoid(gate)), written as bf16 (RNE) or fp32; gw holds
+// the gate's bf16 values of dims d0 .. d0 + 3 when has_gate.
+__device__ __forceinline__ void write_out(void* out, int out_bf16, size_t row_off, int d0, bool has_gate,
+                                          uint2 gw, int gate_ref, float L, const float (&A)[4]) {
     const float inv = __builtin_amdgcn_rcpf(L);
     float o[4] = {A[0] * inv, A[1] * inv, A[2] * inv, A[3] * inv};
-    if (gate_row) {
-        const uint2 gw = *reinterpret_cast<const uint2*>(gate_row + d0);
+    if (has_gate) {
         o[0] *= gate_sigmoid(bf16lo(gw.x), gate_ref);
         o[1] *= gate_sigmoid(bf16hi(gw.x), gate_ref);
         o[2] *= gate_sigmoid(bf16lo(gw.y), gate_ref);
@@ -630,9 +630,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
         d0 = dpart * (kHeadDim / NP) + dl * 4;
     }
     const size_t orow = ((size_t)s * kQHeads + h * kGroup + g) * kHeadDim;
-    const uint16_t* grow = a.gate ? a.gate + orow : nullptr;
+    const bool has_gate = a.gate != nullptr;
+    uint2 gw = make_uint2(0u, 0u);  // gate words of this thread's dims
     if (n_chunks == 1) {
-        if (act) write_out(a.out, a.out_bf16, orow, d0, grow, a.gate_ref, Lsum, A);
+        if (has_gate && act) gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+        if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lsum, A);
         return;
     }
     // Wave g publishes q head g's (m, l, acc) with agent-coherent stores;
@@ -664,6 +666,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     int32_t* ctr = a.counters + (((s * kKvHeads + h) * kMaxDParts + dpart) * kGroup + g) * kCounterStride;
     int prev = 0;
     if (lane == 0) prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the gate words ride along with the arrival: requested after it, they
+    // arrive while it completes, so a combiner does not wait on them after
+    // its fold and no wave waits on them before its arrival
+    asm volatile("" ::: "memory");
+    if (has_gate && act) gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
     if (__builtin_amdgcn_readfirstlane(prev) != n_chunks - 1) return;
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (NP == 1) {
@@ -730,7 +737,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; j++) Ac[j] = sum_xor32(Ac[j]);
     }
-    if (act) write_out(a.out, a.out_bf16, orow, d0, grow, a.gate_ref, Lc, Ac);
+    if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lc, Ac);
     if (lane == 0) *ctr = 0;
 }
 

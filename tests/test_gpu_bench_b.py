@@ -1,11 +1,12 @@
 """The headline benchmark's launches (bench.py config b), checked as timed:
 bench.DecodeB builds the same context, replicas, buffers and HIP graphs the
 bench replays (1 sequence per replica at 4095 tokens, 8 layers, automatic
-chunk and output-dim split, fused 1-token append, bf16 output, a round graph
-over 4 replicas).  After warm-up rounds, one round is replayed and every
-layer's output of every replica is compared with the oracle over the
-4096 keys gathered back from the pool, and the appended slot with the
-appended rows, bit for bit.  The read-floor leg's checksum launches are
+chunk and output-dim split, fused 1-token append, the reference's gate
+sigma(gate) * attention, bf16 output, a round graph over 4 replicas).  After
+warm-up rounds, one round is replayed and every layer's output of every
+replica is compared with the oracle (reference gate) over the 4096 keys
+gathered back from the pool, and the appended slot with the appended rows,
+bit for bit.  The read-floor leg's checksum launches are
 checked against the same gathered keys."""
 import numpy as np
 import pytest
@@ -31,6 +32,7 @@ def test_headline_decode_launch_as_benched():
         q = B.q.download(np.uint16, (n, NQ, D))
         kn = B.kn.download(np.uint16, (n, ROW))
         vn = B.vn.download(np.uint16, (n, ROW))
+        gate = B.gate.download(np.uint16, (n, NQ, D))
         out = O.bf16_to_f32(B.out.download(np.uint16, (n, NQ, D)))
         caches = {}
         for r in range(reps):
@@ -40,11 +42,11 @@ def test_headline_decode_launch_as_benched():
                 # the fused append wrote this step's rows into slot L - 1
                 assert np.array_equal(k[L - 1], kn[i]) and np.array_equal(v[L - 1], vn[i]), (r, layer)
                 caches[(r, layer)] = (k, v)
-        refs = O.decode_attn_batch(q.reshape(n, NQ * D), [caches[(i // layers, i % layers)][0] for i in range(n)],
-                                   [caches[(i // layers, i % layers)][1] for i in range(n)], [L] * n)
         for i in range(n):
-            O.assert_attn_close(out[i], refs[i], what=f"replica {i // layers} layer {i % layers}")
-            O.assert_attn_close(out[i], refs[i], rel_rms=5e-3, what=f"replica {i // layers} layer {i % layers} tight")
+            k, v = caches[(i // layers, i % layers)]
+            ref = O.decode_attn(q[i], k, v, L, gate=gate[i], gate_mode=1)
+            O.assert_attn_close(out[i], ref, what=f"replica {i // layers} layer {i % layers}")
+            O.assert_attn_close(out[i], ref, rel_rms=5e-3, what=f"replica {i // layers} layer {i % layers} tight")
         B.end_round()
         # the floor leg's checksum launches read exactly these keys
         B.run_floor(1)
