@@ -1436,9 +1436,10 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
 //     3-row window in registers.
 // Per token: conv + SiLU -> LDS, barrier; q, k L2-normalised; decay and beta;
 // the delta rule row by row (S *= decay; S += k beta (v_i - S.k); o_i = S.q *
-// scale); barrier; gated RMSNorm with SiLU(z).  exp, sigmoid and SiLU use the
-// hardware units (dn_exp and friends below) where the reference uses
-// Schraudolph approximations (src/engine.cpp:2349-2374).  Two kernels share the row arithmetic (dn_row),
+// scale); barrier; gated RMSNorm with SiLU(z).  beta, SiLU and the softplus
+// exp follow the reference's Schraudolph forms by default (dn_gates,
+// dn_silu below), the hardware units with KVC_FLAG_EXACT_MATH.  Two kernels
+// share the row arithmetic (dn_row),
 // so a token gives the same bits through either: deltanet_kernel keeps both
 // state slabs in registers across a chunk of tokens; deltanet_decode_kernel
 // (one token) streams the rows -- loaded ahead, stored as soon as updated.
@@ -2291,7 +2292,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
     conv_done();
 }
 
-constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel
+constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel (6 and 8 measured slower)
 
 template <bool BF16IN, bool REF>
 __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArgs a) {
