@@ -858,6 +858,69 @@ def run_a(args):
             "finite": bool(np.isfinite(out).all()), "fill_ms": round((t1 - t0) * 1e3, 1)}
 
 
+PHASE_POINTS = ["entry", "walk done", "merge done", "stores complete", "atomic returned", "partials loaded",
+                "folded", "output written"]
+
+
+def run_phases(args, launches=40):
+    """Config b's launch with the decode kernel's phase stamps (the
+    KVC_PHASE_STAMPS build, libkvc_phases.so): per point, the mean and max
+    over workgroups of the time since the launch's first workgroup entered,
+    averaged over `launches` launches.  Each launch is the last layer of a
+    one-replica graph of 8 layers, so it follows 7 launches as in the bench.
+    Points 5-7 are the combining waves' (the last arrival of each (kv head,
+    part, q head)); points 0-4 are every wave's.  `combining_waves` gives
+    every point for those waves alone."""
+    import ctypes
+    import kvc
+
+    B = DecodeB(reps=args.replicas, chunk_blocks=args.chunk_blocks)
+    h = B.h
+    try:
+        L = kvc.lib()
+        buf, wgs, waves, pts = ctypes.c_void_p(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        rc = L.kvc_phase_stamps(ctypes.byref(buf), ctypes.byref(wgs), ctypes.byref(waves), ctypes.byref(pts))
+        if rc:
+            raise RuntimeError(f"kvc_phase_stamps failed ({rc})")
+        nw, nv, npt = wgs.value, waves.value, pts.value
+        stamps = kvc.DeviceBuffer(h, buf.value, nw * nv * npt * 8)  # a device symbol: never freed
+        B.run_steps(args.warmup)
+        h.stream_sync(B.stream)
+        rows = {p: [] for p in PHASE_POINTS}
+        crows = {p: [] for p in PHASE_POINTS}
+        for it in range(launches):
+            r = it % B.reps
+            stamps.zero()
+            h.sync()
+            B.begin_round([B.seqs[r]])
+            h.graph_launch(B.single[r], B.stream)
+            B.end_round([B.seqs[r]])
+            h.stream_sync(B.stream)
+            t = stamps.download(np.uint64, (nw, nv, npt)).astype(np.int64)
+            live = t[:, :, 0] > 0
+            t0 = t[:, :, 0][live].min()
+            us = (t - t0) * 0.01  # 100 MHz counter
+            # points 5-7 of waves that combined in an earlier launch of the
+            # graph are stale: this launch's lie at or after the wave's point 4
+            comb = live & (t[:, :, 7] >= t[:, :, 4]) & (t[:, :, 5] >= t[:, :, 4])
+            for i, p in enumerate(PHASE_POINTS):
+                sel = live & (t[:, :, i] >= t[:, :, 4]) if i > 4 else live
+                if sel.any():
+                    rows[p].append((us[:, :, i][sel].mean(), us[:, :, i][sel].max(), int(sel.sum())))
+                if comb.any():
+                    crows[p].append((us[:, :, i][comb].mean(), us[:, :, i][comb].max(), int(comb.sum())))
+    finally:
+        B.close()
+    def summary(rs):
+        return {p: {"mean_us": round(float(np.mean([v[0] for v in rs[p]])), 2),
+                    "max_us": round(float(np.mean([v[1] for v in rs[p]])), 2),
+                    "waves": int(round(np.mean([v[2] for v in rs[p]])))} for p in PHASE_POINTS if rs[p]}
+
+    return {"metric": "decode_kernel phase stamps, config b (libkvc_phases.so)", "launches": launches,
+            "unit": "us since the launch's first workgroup entered", "phases": summary(rows),
+            "combining_waves": summary(crows)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -871,12 +934,20 @@ def main():
     ap.add_argument("--chunk-blocks", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--phases", action="store_true",
+                    help="config b's decode launch with phase stamps (libkvc_phases.so); prints the phase table")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the KV path "
               "shards by sequence or context across GPUs but no multi-GPU run is part of it.",
               file=sys.stderr)
         sys.exit(2)
+    if args.phases:
+        import kvc
+
+        kvc.LIB_PATH = kvc.PKG_DIR / "libkvc_phases.so"
+        print(json.dumps(run_phases(args)), flush=True)
+        return
     runners = {"a": run_a, "c": run_c, "d": run_d, "e": run_e}
     if args.config in ("all", "b"):
         line = run_b(args)

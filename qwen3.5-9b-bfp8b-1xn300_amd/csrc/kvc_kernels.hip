@@ -486,6 +486,30 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
 // the price of a second (L2-served) read of each chunk's K.
 constexpr int kCombineBatch = 32;
 
+// Phase stamps of the decode kernel, compiled in only for the
+// KVC_PHASE_STAMPS build (libkvc_phases.so, read by bench.py --phases): lane 0
+// of each wave writes s_memrealtime (100 MHz) at fixed points into
+// phase_stamps[workgroup][wave][point].  A stamp adds a counter read and one
+// 8-B vector store and skips no work.  Points: 0 entry, 1 block walk done,
+// 2 wave merge done, 3 partial stores complete, 4 arrival atomic returned,
+// 5 partials loaded (combiner), 6 folded (combiner), 7 output written (the
+// wave that writes it: the combiner, or every wave of a one-chunk launch).
+#ifdef KVC_PHASE_STAMPS
+constexpr int kStampWgs = 4096, kStampPoints = 8;
+__device__ uint64_t phase_stamps[kStampWgs * kWaves * kStampPoints];
+__device__ __forceinline__ void phase_stamp(int point) {
+    uint64_t t;
+    asm volatile("s_memrealtime %0\n\ts_waitcnt lgkmcnt(0)" : "=s"(t)::"memory");
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < kStampWgs)
+        phase_stamps[(blockIdx.x * kWaves + (threadIdx.x >> 6)) * kStampPoints + point] = t;
+}
+#define KVC_STAMP(P) phase_stamp(P)
+#define KVC_STAMP_WAIT_LOADS() asm volatile("s_waitcnt vmcnt(0)" ::: "memory")
+#else
+#define KVC_STAMP(P) ((void)0)
+#define KVC_STAMP_WAIT_LOADS() ((void)0)
+#endif
+
 __device__ __forceinline__ float wave_max(float x) {
     x = fmaxf(x, dpp<kDppXor1>(x));
     x = fmaxf(x, dpp<kDppXor2>(x));
@@ -538,6 +562,7 @@ __device__ __forceinline__ void combine_batch(__amdgpu_buffer_rsrc_t prs, int it
 template <int NP>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     __shared__ DecodeSmem sm;
+    KVC_STAMP(0);
     constexpr int kLanesD = 64 / NP;  // lanes per token subset
     const int b = blockIdx.x;
     const int item = (b & 7) * a.per_xcd + (b >> 3);
@@ -580,6 +605,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
             append_new_token(const_cast<uint16_t*>(a.kpool), const_cast<uint16_t*>(a.vpool), trow, h, new_pos,
                              knew, vnew);
     }
+    KVC_STAMP(1);
 
     const int t = threadIdx.x, g = t >> 6;
     float M, Lsum, A[4];
@@ -629,12 +655,17 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
         }
         d0 = dpart * (kHeadDim / NP) + dl * 4;
     }
+    KVC_STAMP(2);
     const size_t orow = ((size_t)s * kQHeads + h * kGroup + g) * kHeadDim;
     const bool has_gate = a.gate != nullptr;
     uint2 gw = make_uint2(0u, 0u);  // gate words of this thread's dims
     if (n_chunks == 1) {
         if (has_gate && act) gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
         if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lsum, A);
+#ifdef KVC_PHASE_STAMPS
+        __builtin_amdgcn_s_waitcnt(0);
+        KVC_STAMP(7);
+#endif
         return;
     }
     // Wave g publishes q head g's (m, l, acc) with agent-coherent stores;
@@ -661,6 +692,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
         __builtin_amdgcn_raw_buffer_store_b64(mlv, prs, ibase + (kGroup * kHeadDim + 2 * g) * 4, 0, kCpolSC1);
     }
     __builtin_amdgcn_s_waitcnt(0);
+    KVC_STAMP(3);
     // one 128-B line per counter: arrivals on different counters do not
     // contend for one line
     int32_t* ctr = a.counters + (((s * kKvHeads + h) * kMaxDParts + dpart) * kGroup + g) * kCounterStride;
@@ -671,7 +703,9 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     // its fold and no wave waits on them before its arrival
     asm volatile("" ::: "memory");
     if (has_gate && act) gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
-    if (__builtin_amdgcn_readfirstlane(prev) != n_chunks - 1) return;
+    const bool last = __builtin_amdgcn_readfirstlane(prev) == n_chunks - 1;
+    KVC_STAMP(4);
+    if (!last) return;
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
     if constexpr (NP == 1) {
         // combine the n_chunks partials of (s, h): wave g takes q head g; every
@@ -708,6 +742,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
                     prs, ((first + cc * NP) * kItemFloats + g * kHeadDim + dl * 4) * 4, 0, kCpolSC1);
             }
             __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
+            if (k0 == 0) {
+                KVC_STAMP_WAIT_LOADS();
+                KVC_STAMP(5);
+            }
             const bool own = lane < nk;
             const float m_l = own ? __uint_as_float(ml[0]) : kNegBig;
             const float mb = fmaxf(Mc, wave_max(m_l));
@@ -737,8 +775,13 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; j++) Ac[j] = sum_xor32(Ac[j]);
     }
+    KVC_STAMP(6);
     if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lc, Ac);
     if (lane == 0) *ctr = 0;
+#ifdef KVC_PHASE_STAMPS
+    __builtin_amdgcn_s_waitcnt(0);
+    KVC_STAMP(7);
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -2632,6 +2675,18 @@ int launch_decode(const DecodeArgs& a, void* stream) {
         hipLaunchKernelGGL(decode_kernel<1>, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
+
+#ifdef KVC_PHASE_STAMPS
+// Device address and shape of the decode phase stamps (this build only).
+extern "C" __attribute__((visibility("default"))) int kvc_phase_stamps(void** buf, int32_t* wgs, int32_t* waves,
+                                                                     int32_t* points) {
+    if (!buf || !wgs || !waves || !points) return (int)hipErrorInvalidValue;
+    *wgs = kStampWgs;
+    *waves = kWaves;
+    *points = kStampPoints;
+    return (int)hipGetSymbolAddress(buf, HIP_SYMBOL(phase_stamps));
+}
+#endif
 
 int launch_checksum(const ChecksumArgs& a, void* stream) {
     hipLaunchKernelGGL(checksum_kernel, dim3((unsigned)a.n_units), dim3(256), 0, (hipStream_t)stream, a);
