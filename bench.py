@@ -352,9 +352,9 @@ def _oracle():
 
 
 def cpu_baseline_c(P, n_q=128):
-    """Config c on the oracle, bounded samples: the gather as memcpy of the
-    reused K/V (1 thread, 8 sessions), the causal prefill of one session per
-    core (threads), and the producer (q/k RMSNorm + RoPE) of 256 tokens."""
+    """Config c on the oracle: the append and the gather as rates over 8
+    sessions (1 thread), the causal prefill of all 64 sessions of one layer
+    (threads), and the producer (q/k RMSNorm + RoPE) of 256 tokens."""
     from concurrent.futures import ThreadPoolExecutor
 
     O = _oracle()
@@ -387,8 +387,9 @@ def cpu_baseline_c(P, n_q=128):
             np.copyto(dst, src)
     g_s = time.perf_counter() - t0
     g_bytes = 2 * 2 * sum(int(p_) for p_ in P[:8]) * ROW * 2
-    # prefill: one session per core, 128 queries over P + 128 keys
-    samp = [int(x) for x in P[:cores]]
+    # prefill: every one of the 64 sessions (128 queries over P + 128 keys),
+    # one session per task on `cores` threads
+    samp = [int(x) for x in P]
     data = [(O.normal_bf16(n_q * NQ * D, SEED + 400 + i), O.normal_bf16((p_ + n_q) * ROW, SEED + 500 + i),
              O.normal_bf16((p_ + n_q) * ROW, SEED + 600 + i)) for i, p_ in enumerate(samp)]
     t0 = time.perf_counter()
@@ -396,7 +397,6 @@ def cpu_baseline_c(P, n_q=128):
         list(ex.map(lambda a: O.prefill_attn(a[1][0], a[1][1], a[1][2], samp[a[0]], n_q), enumerate(data)))
     p_s = time.perf_counter() - t0
     p_flops = float(sum(16384 * (128 * p_ + 8256) for p_ in samp))
-    all_flops = float(sum(16384 * (128 * int(p_) + 8256) for p_ in P))
     # producer: 256 tokens, 1 thread
     row = O.bf16_to_f32(O.normal_bf16(NQ * 2 * D + 2 * ROW, SEED + 700))
     w = np.ones(D, np.float32)
@@ -410,17 +410,17 @@ def cpu_baseline_c(P, n_q=128):
             "append_GBps_1thread": round(a_bytes / a_s / 1e9, 2),
             "gather_GBps": round(g_bytes / g_s / 1e9, 2),
             "prefill_TFLOPs": round(p_flops / p_s / 1e12, 4),
-            "prefill_us_per_layer": round(all_flops / (p_flops / p_s) * 1e6, 1),
+            "prefill_us_per_layer": round(p_s * 1e6, 1),
             "qkv_append_GBps_1thread": round(q_bytes / q_s / 1e9, 3),
-            "sample": f"append of 8 sessions' 128-token chunks (1 thread); gather of 8 sessions (1 thread); oracle causal prefill of {len(samp)} sessions, one per "
-                      f"thread, scaled to the 64 sessions' flops; producer of 256 tokens (1 thread) "
-                      f"({cpu_model()})"}
+            "sample": f"append of 8 sessions' 128-token chunks (1 thread); gather of 8 sessions (1 thread); oracle "
+                      f"causal prefill of all {len(samp)} sessions of one layer on {cores} threads (measured, not "
+                      f"scaled); producer of 256 tokens (1 thread) ({cpu_model()})"}
 
 
 def cpu_baseline_e(n_sessions=64):
     """Config e on the host: the snapshot copy (61 MB per session, 1 thread,
-    4 sessions) and the Gated-DeltaNet resume step on the oracle (one layer of
-    one session per core, threads, scaled to 64 sessions)."""
+    4 sessions) and the Gated-DeltaNet resume legs on the oracle (one layer
+    of all 64 sessions, threads)."""
     from concurrent.futures import ThreadPoolExecutor
 
     O = _oracle()
@@ -436,41 +436,37 @@ def cpu_baseline_e(n_sessions=64):
     rng = np.random.default_rng(SEED + 800)
     w = [(0.5 * rng.standard_normal((4, O.SSM_C))).astype(np.float32), rng.standard_normal(O.SSM_NV).astype(np.float32),
          -rng.uniform(0.05, 1.0, O.SSM_NV).astype(np.float32), np.ones(O.SSM_DV, np.float32)]
-    jobs = [(np.zeros((3, O.SSM_C), np.float32), np.zeros((O.SSM_NV, O.SSM_DV, O.SSM_DK), np.float32),
-             rng.standard_normal(O.SSM_PROJ).astype(np.float32)) for _ in range(cores)]
-    # the chunk leg: the reference runs a prompt chunk token by token
-    # (src/engine.cpp:2600-2716), so a few tokens per session scale exactly
-    n_chunk_tok = 4
-    rows = [rng.standard_normal((n_chunk_tok, O.SSM_PROJ)).astype(np.float32) for _ in range(cores)]
+    # every one of the n_sessions sessions: its conv window, recurrent state
+    # and the projection rows of up to 128 tokens
+    conv = [np.zeros((3, O.SSM_C), np.float32) for _ in range(n_sessions)]
+    state = [np.zeros((O.SSM_NV, O.SSM_DV, O.SSM_DK), np.float32) for _ in range(n_sessions)]
+    rows = [rng.standard_normal((128, O.SSM_PROJ)).astype(np.float32) for _ in range(n_sessions)]
 
-    def chunk(i):
-        cs, st = jobs[i][0], jobs[i][1]
-        for r in rows[i]:
-            O.deltanet_layer_step(cs, st, r, *w)
+    def steps(i, n_tok):
+        for r in rows[i][:n_tok]:
+            O.deltanet_layer_step(conv[i], state[i], r, *w)
+
+    def timed(n_tok):
+        t0 = time.perf_counter()
+        list(ex.map(lambda i: steps(i, n_tok), range(n_sessions)))
+        return time.perf_counter() - t0
 
     with ThreadPoolExecutor(cores) as ex:
         # untimed: pool start, library set-up and the first touch of each
         # session's state (a fresh 2 MiB state costs ~10 ms of page faults)
-        list(ex.map(lambda j: O.deltanet_layer_step(j[0], j[1], j[2], *w), jobs))
-        d_runs = []  # median of 5 one-token passes (one pass is about a millisecond)
-        for _ in range(5):
-            t0 = time.perf_counter()
-            list(ex.map(lambda j: O.deltanet_layer_step(j[0], j[1], j[2], *w), jobs))
-            d_runs.append(time.perf_counter() - t0)
-        d_s = float(np.median(d_runs))
-        t0 = time.perf_counter()
-        list(ex.map(chunk, range(cores)))
-        k_s = time.perf_counter() - t0
-    chunk_us = k_s * (128 / n_chunk_tok) * n_sessions / cores * 1e6
+        timed(1)
+        d_s = float(np.median([timed(1) for _ in range(5)]))  # one pass is a few milliseconds
+        s_s = timed(8)
+        k_s = timed(128)
     return {"kind": "port", "cores": cores,
             "snapshot_GBps_1thread": round(2 * 4 * per_sess / c_s / 1e9, 2),
-            "resume_decode_us_per_layer": round(d_s * n_sessions / cores * 1e6, 1),
-            "resume_short8_us_per_layer": round(chunk_us * 8 / 128, 1),
-            "resume_chunk128_us_per_layer": round(chunk_us, 1),
-            "resume_chunk128_TFLOPs": round(n_sessions * 128 * DN_TOKEN_FLOP / (chunk_us * 1e-6) / 1e12, 5),
-            "sample": f"4 session snapshots copied (1 thread); the oracle's Gated-DeltaNet step of one layer for "
-                      f"{cores} sessions, one per thread, for 1 token (median of 5 passes) and for {n_chunk_tok} "
-                      f"consecutive tokens, scaled to {n_sessions} sessions and 128 tokens ({cpu_model()})"}
+            "resume_decode_us_per_layer": round(d_s * 1e6, 1),
+            "resume_short8_us_per_layer": round(s_s * 1e6, 1),
+            "resume_chunk128_us_per_layer": round(k_s * 1e6, 1),
+            "resume_chunk128_TFLOPs": round(n_sessions * 128 * DN_TOKEN_FLOP / k_s / 1e12, 5),
+            "sample": f"4 session snapshots copied (1 thread); the oracle's Gated-DeltaNet step of one layer for all "
+                      f"{n_sessions} sessions on {cores} threads, for 1 token (median of 5 passes), 8 tokens and 128 "
+                      f"tokens (measured, not scaled) ({cpu_model()})"}
 
 
 def run_d(args):
