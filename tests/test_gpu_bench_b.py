@@ -58,3 +58,30 @@ def test_headline_decode_launch_as_benched():
                 assert np.array_equal(got[r, layer], O.kv_checksums(*caches[(r, layer)])), (r, layer)
     finally:
         B.close()
+
+
+def test_phase_stamps_build_runs():
+    """bench.py --config b --phases (the KVC_PHASE_STAMPS build,
+    libkvc_phases.so) in a child process, since this one has libkvc.so
+    loaded: every wave stamps points 0-4 in order, and exactly the 32 waves
+    that combine (4 kv heads x 2 parts x 4 q heads) stamp points 5-7, in order."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(bench.__file__).resolve().parent
+    if not (root / "qwen3.5-9b-bfp8b-1xn300_amd" / "libkvc_phases.so").exists():
+        pytest.skip("libkvc_phases.so not built")
+    say("bench.py --config b --phases in a child process")
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--config", "b", "--phases", "--no-cpu",
+                        "--warmup", "8"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    allw, comb = d["phases"], d["combining_waves"]
+    names = bench.PHASE_POINTS
+    assert [allw[p]["waves"] for p in names[:5]] == [1024] * 5
+    assert all(comb[p]["waves"] == 32 for p in names)
+    means = [comb[p]["mean_us"] for p in names]
+    assert all(a <= b for a, b in zip(means, means[1:])), means
+    assert 0 <= means[0] < means[-1] < 100, means
