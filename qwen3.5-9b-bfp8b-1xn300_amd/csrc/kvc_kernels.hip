@@ -2335,7 +2335,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
     conv_done();
 }
 
-constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel (6 and 8 measured slower)
+constexpr int kDnPf = 4;  // rows loaded ahead in the streaming kernel (2, 6 and 8 measured slower)
 
 template <bool BF16IN, bool REF>
 __global__ __launch_bounds__(kDnThreads) void deltanet_decode_kernel(DeltaNetArgs a) {
