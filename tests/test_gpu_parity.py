@@ -83,6 +83,35 @@ def test_append_gather_bitexact():
                 assert np.array_equal(k, mk[37:87]) and np.array_equal(v, mv[37:87])
 
 
+def test_append_gather_remainders():
+    """Append moves 4 tokens per workgroup and gather 16-token halves of
+    32-token chunks: chunks of 1, 2, 3, 5, 6 and 7 tokens leave every
+    remainder of the 4-token groups, at start positions of every residue mod
+    4 and across block edges; gathers of 1, 2, 15, 16, 17, 31, 32 and 33 keys
+    from odd starts end inside, at and past a half or a chunk."""
+    say("append/gather remainders: 1-7 token chunks, short and unaligned gathers")
+    with make_ctx() as ctx:
+        m = Mirror(LAYERS)
+        seqs = [ctx.seq_create() for _ in range(3)]
+        seed = 4000
+        for c in [1, 2, 3, 5, 6, 7, 3, 2, 7, 5, 6, 1, 3, 7, 2, 6, 5, 3]:
+            fill_seq(ctx, m, seqs, c, seed=seed)
+            seed += 17
+        lens = [ctx.seq_len(s) for s in seqs]
+        assert lens == [74] * 3
+        for layer in range(LAYERS):
+            got = gather(ctx, layer, seqs, lens)
+            for s, (k, v) in zip(seqs, got):
+                mk, mv = m.get(s, layer)
+                assert np.array_equal(k, mk) and np.array_equal(v, mv), (s, layer)
+            for tok0, n in [(0, 1), (5, 2), (1, 15), (3, 16), (13, 17), (31, 31), (33, 32), (7, 33), (39, 33)]:
+                got = gather(ctx, layer, seqs, [n] * 3, tok0=tok0)
+                for s, (k, v) in zip(seqs, got):
+                    mk, mv = m.get(s, layer)
+                    assert np.array_equal(k, mk[tok0:tok0 + n]) and np.array_equal(v, mv[tok0:tok0 + n]), \
+                        (s, layer, tok0, n)
+
+
 @pytest.mark.parametrize("L", [1, 33, 257])
 def test_decode_matches_golden(golden_dir, L):
     g = np.load(golden_dir / "attention_golden.npz")
