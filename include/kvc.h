@@ -212,12 +212,12 @@ int kvc_decode_attn(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
  * harnesses that forbid hipMalloc): same arguments, semantics and results
  * (bit for bit: same work split and kernels), but the split-K partials and
  * arrival counters live in the library's static per-GPU workspace -- a
- * file-scope __device__ array of 2048 split-K items plus counters, 8.9 MB,
+ * file-scope __device__ array of 4096 split-K items plus counters, 17.6 MB,
  * held by each GPU the library runs on until the process ends -- instead of
  * the context's.  The call allocates nothing.  A launch needing more than
- * 2048 items (chunks x kv heads x output-dim parts) is refused with
- * KVC_ERR_RANGE before anything runs; the automatic split stays within
- * ~1100 items for 64 sequences of any length.  Every call on one GPU shares
+ * 4096 items (chunks x kv heads x output-dim parts) is refused with
+ * KVC_ERR_RANGE before anything runs; the automatic split (decode_chunk_blocks
+ * = 0) never needs more, for 64 sequences of any length.  Every call on one GPU shares
  * that workspace: calls that overlap on one GPU (other streams, other
  * contexts, other host threads) race and must be serialised by the caller. */
 int kvc_decode_attn_static(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,

@@ -1087,16 +1087,14 @@ int kvc_qkv_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seq
 // dims over 2 workgroups (one per CU of the 256 is the aim).
 constexpr int64_t kDsplitBelowItems = 256;
 
-static int32_t auto_chunk_blocks(kvc_ctx* c, int64_t total_blocks, int64_t max_items) {
+static int32_t auto_chunk_blocks(kvc_ctx* c, int64_t total_blocks) {
     if (c->cfg.decode_chunk_blocks > 0) return c->cfg.decode_chunk_blocks;
-    // About 16 items per CU on 256 CUs (4096, or fewer if the workspace holds
-    // fewer): three decode workgroups are resident per CU, and many short
-    // items balance the ragged sequences' chunks better than a few long ones
-    // (config d: 598-602 us per layer at 3072-6144 items against 627 at 1024).
-    // Chunks of at least 4 blocks keep the split-K partial traffic and the
-    // final combine small.
-    const int64_t target_items = std::min<int64_t>(4096, max_items);
-    int64_t cb = (total_blocks * kKvHeads + target_items - 1) / target_items;
+    // About 16 items per CU on 256 CUs (kAutoItems): three decode workgroups
+    // are resident per CU, and many short items balance the ragged sequences'
+    // chunks better than a few long ones (config d: 598-602 us per layer at
+    // 3072-6144 items against 627 at 1024).  Chunks of at least 4 blocks keep
+    // the split-K partial traffic and the final combine small.
+    int64_t cb = (total_blocks * kKvHeads + kAutoItems - 1) / kAutoItems;
     return (int32_t)std::max<int64_t>(4, cb);
 }
 
@@ -1122,7 +1120,7 @@ static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int
         a.kv_len[j] = L;
         total_blocks += (L + kBlockTok - 1) / kBlockTok;
     }
-    int32_t cb = auto_chunk_blocks(c, total_blocks, max_items);
+    int32_t cb = auto_chunk_blocks(c, total_blocks);
     const bool auto_cb = c->cfg.decode_chunk_blocks <= 0;
     const bool force_split = c->cfg.flags & KVC_FLAG_DECODE_SPLIT_D;
     const int64_t max_chunks = force_split ? kMaxChunks / kMaxDParts : kMaxChunks;
@@ -1134,10 +1132,11 @@ static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int
             const int32_t nb = (a.kv_len[j] + kBlockTok - 1) / kBlockTok;
             total_chunks += (nb + cb - 1) / cb;
         }
-        // an automatic chunk also grows until the launch fits the workspace
-        // (each sequence's last, partial chunk adds an item per kv head); a
-        // chunk size the caller set is kept and checked below
-        if (total_chunks <= max_chunks && (!auto_cb || total_chunks * kKvHeads <= max_items)) break;
+        // an automatic chunk also grows until the launch has at most
+        // kAutoItems items (each sequence's last, partial chunk adds one per
+        // kv head), the same in either workspace; a chunk size the caller set
+        // is kept and checked below
+        if (total_chunks <= max_chunks && (!auto_cb || total_chunks * kKvHeads <= kAutoItems)) break;
         cb *= 2;
     }
     int32_t d_parts = 1;

@@ -44,8 +44,12 @@ constexpr size_t kCounterBytes = (size_t)kMaxBatch * kKvHeads * kMaxDParts * kGr
 // Static workspace of kvc_decode_attn_static, the entry point that allocates
 // nothing: a file-scope __device__ array of this many split-K items (plus the
 // arrival counters) per GPU, held until the process ends.
-constexpr int kStaticItems = 2048;
-constexpr size_t kStaticPartBytes = (size_t)kStaticItems * kItemFloats * 4;  // 8,650,752 B (+ 256 KiB counters)
+constexpr int kStaticItems = 4096;
+constexpr size_t kStaticPartBytes = (size_t)kStaticItems * kItemFloats * 4;  // 17,301,504 B (+ 256 KiB counters)
+// The automatic split-K chunk keeps a launch within this many items, in both
+// workspaces, so kvc_decode_attn and kvc_decode_attn_static take the same
+// split whenever the caller leaves decode_chunk_blocks at 0.
+constexpr int kAutoItems = kStaticItems;
 constexpr int kMaxDevices = 64;
 constexpr int kTableUpdatesPerLaunch = 480;
 

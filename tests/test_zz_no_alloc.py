@@ -1,7 +1,7 @@
 """kvc_decode_attn_static: decode attention that allocates nothing, for
 callers that cannot call hipMalloc (HIP graph capture, tight serving loops).
 Its split-K partials and arrival counters live in a file-scope __device__
-array of the library (kStaticItems = 2048 items plus counters, 8.9 MB per GPU) instead of
+array of the library (kStaticItems = 4096 items plus counters, 17.6 MB per GPU) instead of
 the context's workspace.  Through the C ABI, on two calls in a row (the
 second smaller), its output must equal kvc_decode_attn's bit for bit: both
 take the same work split and kernels.  A call that needs more split-K items
@@ -98,14 +98,15 @@ def _new_rows(seed, n, i):
 
 
 def test_static_decode_limit():
-    """decode_chunk_blocks = 2 over a 32768-token sequence is 512 chunks x 4
-    kv heads = 2048 items: the static array's limit, accepted and equal to the
-    regular call.  With 1-block chunks it needs 4096 and is refused."""
-    say("static-workspace decode at and beyond its 2048-item limit")
+    """decode_chunk_blocks = 1 over a 32768-token sequence is 1024 chunks x 4
+    kv heads = 4096 items: the static array's limit, accepted and equal to
+    the regular call.  With the output-dim split forced on it needs 8192 and
+    is refused (the context's own workspace holds it)."""
+    say("static-workspace decode at and beyond its 4096-item limit")
     h = kvc.hip()
-    for cb, ok in ((2, True), (1, False)):
+    for flags, ok in ((0, True), (kvc.FLAG_DECODE_SPLIT_D, False)):
         with kvc.Context(n_attn_layers=1, n_ssm_layers=0, max_seqs=2, max_seq_len=32768, pool_blocks=1100,
-                         snapshot_slots=0, alloc_seed=78, decode_chunk_blocks=cb) as ctx:
+                         snapshot_slots=0, alloc_seed=78, decode_chunk_blocks=1, flags=flags) as ctx:
             ctx.pool_fill_normal(79)
             s = ctx.seq_create()
             ctx.reserve([s], 32768)
@@ -121,9 +122,37 @@ def test_static_decode_limit():
             else:
                 assert rc == kvc.KVC_ERR_RANGE
                 msg = kvc.lib().kvc_last_error().decode()
-                assert "4096 split-K items" in msg and "2048" in msg, msg
+                assert "8192 split-K items" in msg and "4096" in msg, msg
                 ctx.decode_attn(0, [s], q, o1)  # the context's own workspace holds it
                 ctx.sync()
                 assert np.isfinite(o1.download(np.float32, (NQ * D,))).all()
             for b in (q, o1, o2):
                 b.free()
+
+
+def test_static_decode_auto_split_large_batch():
+    """With the automatic chunk, a batch large enough to reach the split's
+    4096-item cap (16 sequences of 16384 tokens: 8-block chunks) takes the
+    same split in both workspaces: the static call equals the regular one
+    bit for bit."""
+    say("static vs regular decode, automatic split at its 4096-item cap, 16 x 16384 tokens")
+    h = kvc.hip()
+    n, L = 16, 16384
+    with kvc.Context(n_attn_layers=1, n_ssm_layers=0, max_seqs=n, max_seq_len=L, pool_blocks=n * L // 32 + 16,
+                     snapshot_slots=0, alloc_seed=81) as ctx:
+        ctx.pool_fill_normal(82)
+        seqs = [ctx.seq_create() for _ in range(n)]
+        ctx.reserve(seqs, L)
+        ctx.commit(seqs, L)
+        q = kvc.to_device(O.normal_bf16(n * NQ * D, 83))
+        gate = kvc.to_device(O.normal_bf16(n * NQ * D, 84))
+        o1, o2 = h.malloc(n * NQ * D * 2), h.malloc(n * NQ * D * 2)
+        ctx.decode_attn(0, seqs, q, o1, gate=gate, out_dtype=kvc.DTYPE_BF16)
+        rc = call_static(ctx, 0, seqs, q, o2, gate=gate, out_dtype=kvc.DTYPE_BF16)
+        assert rc == kvc.KVC_OK, kvc.lib().kvc_last_error()
+        ctx.sync()
+        a, b = o1.download(np.uint16, (n, NQ, D)), o2.download(np.uint16, (n, NQ, D))
+        assert np.array_equal(a, b)
+        assert np.isfinite(O.bf16_to_f32(a)).all()
+        for b_ in (q, gate, o1, o2):
+            b_.free()
