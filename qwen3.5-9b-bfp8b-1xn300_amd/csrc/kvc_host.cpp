@@ -1290,7 +1290,7 @@ int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
         a.out_begin[n] = (int32_t)tot;
         a.item_begin[n] = (int32_t)items;
         a.n_items = (int32_t)items;
-        if (items * 8 * 256 > (int64_t)UINT32_MAX) return set_err(KVC_ERR_RANGE, "gather too large");
+        if (items * kGatherWgsPerItem * 256 > (int64_t)UINT32_MAX) return set_err(KVC_ERR_RANGE, "gather too large");
         a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
         a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
         a.table = c->d_table;

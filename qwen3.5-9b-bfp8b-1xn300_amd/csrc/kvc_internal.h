@@ -44,6 +44,9 @@ constexpr size_t kCounterBytes = (size_t)kMaxBatch * kKvHeads * kMaxDParts * kGr
 // Static workspace of kvc_decode_attn_static, the entry point that allocates
 // nothing: a file-scope __device__ array of this many split-K items (plus the
 // arrival counters) per GPU, held until the process ends.
+// gather: workgroups per 32-token work item = (K or V) x kGatherQ parts
+constexpr int kGatherQ = 2;
+constexpr int kGatherWgsPerItem = 2 * kGatherQ;
 constexpr int kStaticItems = 4096;
 constexpr size_t kStaticPartBytes = (size_t)kStaticItems * kItemFloats * 4;  // 17,301,504 B (+ 256 KiB counters)
 // The automatic split-K chunk keeps a launch within this many items, in both

@@ -2423,10 +2423,9 @@ __global__ __launch_bounds__(256) void zero_state_kernel(ZeroStateArgs a) {
 // Pool reads are plain loads, output stores non-temporal: for config c's
 // 16 x 8192 tokens x 8 layers, 8-token quarters with non-temporal loads ran
 // 157 us, 16-token halves with plain loads run 127 us.
-constexpr int kGatherQ = 2;                          // workgroups per 32-token chunk and K|V
-constexpr int kGatherTok = kBlockTok / kGatherQ;     // tokens per workgroup
+constexpr int kGatherTok = kBlockTok / kGatherQ;     // tokens per workgroup (kGatherQ per chunk and K|V)
 __global__ __launch_bounds__(256) void gather_kernel(GatherArgs a) {
-    const int item = blockIdx.x / (2 * kGatherQ);
+    const int item = blockIdx.x / kGatherWgsPerItem;
     const int kv = (blockIdx.x / kGatherQ) & 1, q8 = blockIdx.x % kGatherQ;
     int s = 0;
     while (s + 1 < a.n_seqs && a.item_begin[s + 1] <= item) s++;
@@ -2770,7 +2769,8 @@ int launch_zero_state(const ZeroStateArgs& a, void* stream) {
 
 int launch_gather(const GatherArgs& a, void* stream) {
     if (a.n_items <= 0) return 0;
-    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)a.n_items * 2 * kGatherQ), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(gather_kernel, dim3((unsigned)a.n_items * kGatherWgsPerItem), dim3(256), 0, (hipStream_t)stream,
+                       a);
     return (int)hipGetLastError();
 }
 
