@@ -282,6 +282,74 @@ def test_prefill_batch_vs_oracle():
             O.assert_attn_close(out[i], ref, rel_rms=3e-3, what='tight')
 
 
+def test_calls_beyond_one_launch():
+    """A call over more sequences than one launch's argument block holds (64)
+    runs as several launches: 70 ragged sequences through one append call,
+    gather, per-unit checksums, a gated decode with fused append (bf16 out)
+    and a 16-row prefill chunk, each against the mirror or the oracle."""
+    say("70 sequences per call: append, gather, checksum, decode, prefill")
+    n, n_q = 70, 16
+    rng = np.random.default_rng(7070)
+    extra = [int(x) for x in rng.integers(0, 200, n)]
+    h = kvc.hip()
+    with make_ctx(max_seqs=n, pool_blocks=2048) as ctx:
+        m = Mirror(1)
+        seqs = [ctx.seq_create() for _ in range(n)]
+        fill_seq(ctx, m, seqs, 20, seed=7100, layers=[0])  # one append call over all 70
+        for s, e in zip(seqs, extra):  # ragged lengths
+            if e:
+                fill_seq(ctx, m, [s], e, seed=7200 + 7 * s, layers=[0])
+        lens = [ctx.seq_len(s) for s in seqs]
+        assert lens == [20 + e for e in extra]
+        got = gather(ctx, 0, seqs, lens)
+        for s, (k, v) in zip(seqs, got):
+            mk, mv = m.get(s, 0)
+            assert np.array_equal(k, mk) and np.array_equal(v, mv), s
+        units = [(L + BT - 1) // BT * 2 * NKV for L in lens]
+        cb = h.malloc(8 * sum(units))
+        ctx.kv_checksum(0, seqs, cb)
+        ctx.sync()
+        sums = cb.download(np.uint64, (sum(units),))
+        cb.free()
+        o = 0
+        for s, u in zip(seqs, units):
+            assert np.array_equal(sums[o:o + u], O.kv_checksums(*m.get(s, 0))), s
+            o += u
+        # gated decode with the fused append of one new token per sequence
+        q = O.normal_bf16(n * NQ * D, 7300).reshape(n, NQ, D)
+        gate = O.normal_bf16(n * NQ * D, 7301).reshape(n, NQ, D)
+        kn = O.normal_bf16(n * ROW, 7302).reshape(n, ROW)
+        vn = O.normal_bf16(n * ROW, 7303).reshape(n, ROW)
+        ctx.reserve(seqs, 1)
+        out = run_decode(ctx, 0, seqs, q, k_new=kn, v_new=vn, gate=gate, out_dtype=kvc.DTYPE_BF16)
+        ctx.commit(seqs, 1)
+        for i, s in enumerate(seqs):
+            m.append(s, 0, kn[i], vn[i])
+            mk, mv = m.get(s, 0)
+            ref = O.decode_attn(q[i], mk, mv, lens[i] + 1, gate=gate[i], gate_mode=1)
+            O.assert_attn_close(out[i], ref, rel_rms=5e-3, what=f"decode seq {i} L={lens[i] + 1}")
+        # a 16-row prefill chunk for every sequence
+        k = O.normal_bf16(n * n_q * ROW, 7401).reshape(n, n_q, ROW)
+        v = O.normal_bf16(n * n_q * ROW, 7402).reshape(n, n_q, ROW)
+        qp = O.normal_bf16(n * n_q * NQ * D, 7403).reshape(n, n_q, NQ, D)
+        ctx.reserve(seqs, n_q)
+        kb, vb, qb = h.malloc(k.nbytes).upload(k), h.malloc(v.nbytes).upload(v), h.malloc(qp.nbytes).upload(qp)
+        ob = h.malloc(n * n_q * NQ * D * 4)
+        ctx.append(0, seqs, n_q, kb, vb)
+        ctx.prefill_attn(0, seqs, n_q, qb, ob)
+        ctx.commit(seqs, n_q)
+        ctx.sync()
+        outp = ob.download(np.float32, (n, n_q, NQ, D))
+        for b in (kb, vb, qb, ob):
+            b.free()
+        for i, s in enumerate(seqs):
+            P = lens[i] + 1
+            m.append(s, 0, k[i], v[i])
+            mk, mv = m.get(s, 0)
+            ref = O.prefill_attn(qp[i], mk, mv, P, n_q)
+            O.assert_attn_close(outp[i], ref, rel_rms=3e-3, what=f"prefill seq {i} P={P}")
+
+
 @pytest.mark.parametrize("split", ["on", "off"])
 def test_splitk_workspace_reuse_stress(split):
     """Many split-K launches back to back on one stream, each with new data in
