@@ -120,6 +120,14 @@ def test_deltanet_single_token_matches_oracle(in_dtype):
     run_case(in_dtype, kvc.DTYPE_F32, n_tok=1, n_seqs=3, seed=7100 + in_dtype)
 
 
+@pytest.mark.parametrize("n_tok", [1, 3, 16])
+def test_deltanet_beyond_one_launch(n_tok):
+    """70 sessions in one call run as launches of at most 64: the streaming
+    one-token kernel (1), the blocked kernel (3) and the matrix form (16)."""
+    say(f"deltanet step, 70 sessions in one call, {n_tok} tokens")
+    run_case(kvc.DTYPE_BF16, kvc.DTYPE_F32, n_tok=n_tok, n_seqs=70, seed=7700 + n_tok)
+
+
 def test_deltanet_chunk_and_bf16_out():
     say("deltanet step, 5-token chunk, bf16 out")
     run_case(kvc.DTYPE_F32, kvc.DTYPE_F32, n_tok=5, n_seqs=2, seed=7200, layer=0)

@@ -127,6 +127,27 @@ def test_snapshot_save_restore_bitexact():
         assert e.value.code == kvc.KVC_ERR_INVALID
 
 
+def test_snapshot_save_restore_beyond_one_launch():
+    """70 sequences saved in one call and restored into 70 fresh sequences in
+    one call (launches of at most 64 sequences): every state and K/V segment
+    comes back bit for bit."""
+    say("snapshot save/restore of 70 sequences per call")
+    n = 70
+    with hybrid_ctx(max_seqs=2 * n, pool_blocks=2 * n * 8 + 64, snapshot_slots=2 * n + 8) as ctx:
+        m = Mirror(LAYERS)
+        seqs = [ctx.seq_create() for _ in range(n)]
+        fill_seq(ctx, m, seqs, 256, seed=300)
+        want = [write_state(ctx, s, 1000 + i) for i, s in enumerate(seqs)]
+        ids = ctx.snapshot_save(seqs)
+        assert len(set(ids)) == n
+        fresh = [ctx.seq_create() for _ in range(n)]
+        ctx.snapshot_restore(fresh, ids)
+        for i, (s, f) in enumerate(zip(seqs, fresh)):
+            assert ctx.seq_len(f) == 256
+            assert_state_equal(read_state(ctx, f), want[i], f"sequence {i}")
+            assert_kv_equal(ctx, f, m, s, 256, f"sequence {i}")
+
+
 def _fill_with_boundary_states(ctx, m, s, tokens, seed, chunk=128):
     """Append `tokens` in chunks; before each commit that lands on a 256
     boundary, write a distinct state (the auto-snapshot then captures it)."""
