@@ -35,7 +35,7 @@ def assert_bf16_close(got, want_f32, what):
 def run_case(rope_dim, in_dtype, prefix, n_tok, seed):
     h = kvc.hip()
     max_len = 2048
-    with kvc.Context(n_attn_layers=2, n_ssm_layers=0, max_seqs=8, max_seq_len=max_len, pool_blocks=512,
+    with kvc.Context(n_attn_layers=2, n_ssm_layers=0, max_seqs=max(8, len(prefix)), max_seq_len=max_len, pool_blocks=512,
                      snapshot_slots=0, alloc_seed=99, rope_dim=rope_dim) as ctx:
         m = Mirror(2)
         seqs = [ctx.seq_create() for _ in prefix]
@@ -95,6 +95,13 @@ def test_qkv_append_rope_widths(rope_dim):
     (16) and across a half-wave (256)."""
     say(f"qkv append, rope_dim={rope_dim}")
     run_case(rope_dim, kvc.DTYPE_F32, prefix=[3, 200], n_tok=9, seed=4500 + rope_dim)
+
+
+def test_qkv_append_beyond_one_launch():
+    """70 sequences in one call (launches of at most 64), ragged prefixes."""
+    say("qkv append, 70 sequences per call")
+    prefix = [int(x) for x in np.random.default_rng(4600).integers(0, 100, 70)]
+    run_case(64, kvc.DTYPE_BF16, prefix=prefix, n_tok=2, seed=4600)
 
 
 def test_qkv_append_feeds_decode():
