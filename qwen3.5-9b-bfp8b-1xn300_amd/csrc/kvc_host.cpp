@@ -1013,6 +1013,7 @@ int kvc_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
         if (c->seqs[seqs[i]].pending < n_tok)
             return set_err(KVC_ERR_STATE, "sequence %d: append of %d tokens but %d reserved", seqs[i], n_tok,
                            c->seqs[seqs[i]].pending);
+    if ((int64_t)std::min(kMaxBatch, n_seqs) * n_tok > INT32_MAX) return set_err(KVC_ERR_RANGE, "append too large");
     const size_t row = (size_t)kKvHeads * kHeadDim;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
         const int32_t n = std::min(kMaxBatch, n_seqs - i0);
@@ -1030,7 +1031,6 @@ int kvc_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
             a.slot[j] = seqs[i0 + j];
             a.pos0[j] = s.len + s.pending - n_tok;
         }
-        if ((int64_t)n * n_tok > INT32_MAX) return set_err(KVC_ERR_RANGE, "append too large");
         int e = launch_append(a, stream);
         if (e) return hip_err((hipError_t)e, "append launch");
     }
@@ -1050,11 +1050,12 @@ int kvc_qkv_append(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seq
         if (c->seqs[seqs[i]].pending < n_tok)
             return set_err(KVC_ERR_STATE, "sequence %d: append of %d tokens but %d reserved", seqs[i], n_tok,
                            c->seqs[seqs[i]].pending);
+    if ((int64_t)std::min(kMaxBatch, n_seqs) * n_tok > INT32_MAX)
+        return set_err(KVC_ERR_RANGE, "qkv append too large");
     const size_t esz = in_dtype == KVC_DTYPE_BF16 ? 2 : 4;
     const size_t qrow = (size_t)kQHeads * kHeadDim;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
         const int32_t n = std::min(kMaxBatch, n_seqs - i0);
-        if ((int64_t)n * n_tok > INT32_MAX) return set_err(KVC_ERR_RANGE, "qkv append too large");
         QkvArgs a{};
         a.qkv = static_cast<const uint8_t*>(qkv) + (size_t)i0 * n_tok * kQkvRow * esz;
         a.q_norm = static_cast<const float*>(q_norm);
@@ -1228,6 +1229,10 @@ int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_s
     if (!q || !out || n_q <= 0) return set_err(KVC_ERR_INVALID, "prefill needs q, out and n_q > 0");
     if (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16) return set_err(KVC_ERR_INVALID, "bad out_dtype");
     if (!std::isfinite(scale)) return set_err(KVC_ERR_INVALID, "scale must be finite");
+    for (int32_t i = 0; i < n_seqs; i++)
+        if (c->seqs[seqs[i]].pending < n_q)
+            return set_err(KVC_ERR_STATE, "sequence %d: prefill of %d rows but %d reserved", seqs[i], n_q,
+                           c->seqs[seqs[i]].pending);
     const size_t qrow = (size_t)n_q * kQHeads * kHeadDim;
     const size_t osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
@@ -1235,9 +1240,6 @@ int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_s
         PrefillArgs a{};
         for (int32_t j = 0; j < n; j++) {
             const Seq& s = c->seqs[seqs[i0 + j]];
-            if (s.pending < n_q)
-                return set_err(KVC_ERR_STATE, "sequence %d: prefill of %d rows but %d reserved", seqs[i0 + j], n_q,
-                               s.pending);
             a.slot[j] = seqs[i0 + j];
             a.q_pos0[j] = s.len + s.pending - n_q;
         }
@@ -1269,6 +1271,18 @@ int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
     int rc;
     if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
     if (!n_tok || !k_out || !v_out || tok0 < 0) return set_err(KVC_ERR_INVALID, "gather needs n_tok and outputs");
+    int64_t batch_items = 0;  // work items of the current launch (one per 32 output tokens)
+    for (int32_t i = 0; i < n_seqs; i++) {
+        const Seq& s = c->seqs[seqs[i]];
+        const int32_t nt = n_tok[i];
+        if (nt < 0 || (int64_t)tok0 + nt > s.len + s.pending)
+            return set_err(KVC_ERR_RANGE, "sequence %d: gather [%d, %d) beyond length %d", seqs[i], tok0, tok0 + nt,
+                           s.len + s.pending);
+        if (i % kMaxBatch == 0) batch_items = 0;
+        batch_items += (nt + kBlockTok - 1) / kBlockTok;
+        if (batch_items * kGatherWgsPerItem * 256 > (int64_t)UINT32_MAX)
+            return set_err(KVC_ERR_RANGE, "gather too large");
+    }
     const size_t row = (size_t)kKvHeads * kHeadDim;
     int64_t out_off = 0;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
@@ -1276,11 +1290,7 @@ int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
         GatherArgs a{};
         int64_t tot = 0, items = 0;
         for (int32_t j = 0; j < n; j++) {
-            const Seq& s = c->seqs[seqs[i0 + j]];
             const int32_t nt = n_tok[i0 + j];
-            if (nt < 0 || (int64_t)tok0 + nt > s.len + s.pending)
-                return set_err(KVC_ERR_RANGE, "sequence %d: gather [%d, %d) beyond length %d", seqs[i0 + j], tok0,
-                               tok0 + nt, s.len + s.pending);
             a.slot[j] = seqs[i0 + j];
             a.out_begin[j] = (int32_t)tot;
             a.item_begin[j] = (int32_t)items;
@@ -1290,7 +1300,6 @@ int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, i
         a.out_begin[n] = (int32_t)tot;
         a.item_begin[n] = (int32_t)items;
         a.n_items = (int32_t)items;
-        if (items * kGatherWgsPerItem * 256 > (int64_t)UINT32_MAX) return set_err(KVC_ERR_RANGE, "gather too large");
         a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
         a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
         a.table = c->d_table;
@@ -1314,6 +1323,13 @@ int kvc_kv_checksum(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
     int rc;
     if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
     if (!out) return set_err(KVC_ERR_INVALID, "checksum needs an output array");
+    int64_t batch_units = 0;  // units of the current launch
+    for (int32_t i = 0; i < n_seqs; i++) {
+        const Seq& s = c->seqs[seqs[i]];
+        if (i % kMaxBatch == 0) batch_units = 0;
+        batch_units += (int64_t)((s.len + s.pending + kBlockTok - 1) / kBlockTok) * 2 * kKvHeads;
+        if (batch_units > INT32_MAX) return set_err(KVC_ERR_RANGE, "checksum too large");
+    }
     int64_t out_off = 0;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
         const int32_t n = std::min(kMaxBatch, n_seqs - i0);
@@ -1328,7 +1344,6 @@ int kvc_kv_checksum(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
             units += (int64_t)((L + kBlockTok - 1) / kBlockTok) * 2 * kKvHeads;
         }
         a.unit_begin[n] = (int32_t)units;
-        if (units > INT32_MAX) return set_err(KVC_ERR_RANGE, "checksum too large");
         a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
         a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
         a.table = c->d_table;

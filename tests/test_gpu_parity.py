@@ -305,6 +305,18 @@ def test_calls_beyond_one_launch():
         for s, (k, v) in zip(seqs, got):
             mk, mv = m.get(s, 0)
             assert np.array_equal(k, mk) and np.array_equal(v, mv), s
+        # a call whose last sequence is out of range fails before any launch:
+        # the outputs of the 64 sequences in its first launch stay untouched
+        bad = lens[:-1] + [lens[-1] + 1]
+        kb_, vb_ = h.malloc(sum(bad) * ROW * 2), h.malloc(sum(bad) * ROW * 2)
+        kb_.upload(np.full(sum(bad) * ROW, 0x7E7E, np.uint16))
+        with pytest.raises(kvc.KvcError) as e:
+            ctx.gather(0, seqs, 0, bad, kb_, vb_)
+        assert e.value.code == kvc.KVC_ERR_RANGE
+        ctx.sync()
+        assert (kb_.download(np.uint16, (sum(bad) * ROW,)) == 0x7E7E).all()
+        kb_.free()
+        vb_.free()
         units = [(L + BT - 1) // BT * 2 * NKV for L in lens]
         cb = h.malloc(8 * sum(units))
         ctx.kv_checksum(0, seqs, cb)
@@ -328,11 +340,24 @@ def test_calls_beyond_one_launch():
             mk, mv = m.get(s, 0)
             ref = O.decode_attn(q[i], mk, mv, lens[i] + 1, gate=gate[i], gate_mode=1)
             O.assert_attn_close(out[i], ref, rel_rms=5e-3, what=f"decode seq {i} L={lens[i] + 1}")
+        # a prefill over sequences of which the last has no reserved rows
+        # fails before any launch
+        qz = h.malloc(n * n_q * NQ * D * 2)
+        oz = h.malloc(n * n_q * NQ * D * 4)
+        oz.upload(np.full(n * n_q * NQ * D, 0x7F7F7F7F, np.uint32))
+        ctx.reserve(seqs[:-1], n_q)
+        with pytest.raises(kvc.KvcError) as e:
+            ctx.prefill_attn(0, seqs, n_q, qz, oz)
+        assert e.value.code == kvc.KVC_ERR_STATE
+        ctx.sync()
+        assert (oz.download(np.uint32, (n * n_q * NQ * D,)) == 0x7F7F7F7F).all()
+        for b in (qz, oz):
+            b.free()
+        ctx.reserve(seqs[-1:], n_q)
         # a 16-row prefill chunk for every sequence
         k = O.normal_bf16(n * n_q * ROW, 7401).reshape(n, n_q, ROW)
         v = O.normal_bf16(n * n_q * ROW, 7402).reshape(n, n_q, ROW)
         qp = O.normal_bf16(n * n_q * NQ * D, 7403).reshape(n, n_q, NQ, D)
-        ctx.reserve(seqs, n_q)
         kb, vb, qb = h.malloc(k.nbytes).upload(k), h.malloc(v.nbytes).upload(v), h.malloc(qp.nbytes).upload(qp)
         ob = h.malloc(n * n_q * NQ * D * 4)
         ctx.append(0, seqs, n_q, kb, vb)
