@@ -1103,10 +1103,17 @@ static int32_t auto_chunk_blocks(kvc_ctx* c, int64_t total_blocks) {
 // pointers.  The split-K partials and arrival counters live in `part` /
 // `counters`; a launch needing more than `max_items` items is refused
 // (KVC_ERR_RANGE).  No allocation.
+// The producer inputs of kvc_decode_step (qkv == nullptr: plain decode).
+struct DecodeProducer {
+    const void* qkv = nullptr;
+    const void* q_norm = nullptr;
+    const void* k_norm = nullptr;
+};
+
 static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t i0, int32_t n, const void* q,
-                             const void* k_new, const void* v_new, const void* gate, void* out, int32_t out_dtype,
-                             float scale, float* part, uint32_t part_bytes, int32_t* counters, int64_t max_items,
-                             const char* workspace, DecodeArgs& a) {
+                             const void* k_new, const void* v_new, const void* gate, const DecodeProducer& prod,
+                             void* out, int32_t out_dtype, float scale, float* part, uint32_t part_bytes,
+                             int32_t* counters, int64_t max_items, const char* workspace, DecodeArgs& a) {
     const size_t qrow = (size_t)kQHeads * kHeadDim, kvrow = (size_t)kKvHeads * kHeadDim;
     const size_t osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
     memset(&a, 0, sizeof a);
@@ -1115,7 +1122,7 @@ static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int
         const Seq& s = c->seqs[seqs[i0 + j]];
         const int32_t L = s.len + s.pending;
         if (L <= 0) return set_err(KVC_ERR_STATE, "sequence %d has no keys to attend", seqs[i0 + j]);
-        if (k_new && s.pending < 1)
+        if ((k_new || prod.qkv) && s.pending < 1)
             return set_err(KVC_ERR_STATE, "sequence %d: fused append needs a reserved token", seqs[i0 + j]);
         a.slot[j] = seqs[i0 + j];
         a.kv_len[j] = L;
@@ -1154,7 +1161,16 @@ static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int
     a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
     a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
     a.table = c->d_table;
-    a.q = static_cast<const uint16_t*>(q) + (size_t)i0 * qrow;
+    if (prod.qkv) {
+        a.qkv = static_cast<const uint16_t*>(prod.qkv) + (size_t)i0 * kQkvRow;
+        a.q_norm = static_cast<const float*>(prod.q_norm);
+        a.k_norm = static_cast<const float*>(prod.k_norm);
+        a.rope = c->d_rope;
+        a.eps = c->cfg.rms_norm_eps;
+        a.rope_half = c->cfg.rope_dim / 2;
+        a.rope_rows = c->cfg.max_seq_len;
+    }
+    a.q = q ? static_cast<const uint16_t*>(q) + (size_t)i0 * qrow : nullptr;
     a.k_new = k_new ? static_cast<const uint16_t*>(k_new) + (size_t)i0 * kvrow : nullptr;
     a.v_new = v_new ? static_cast<const uint16_t*>(v_new) + (size_t)i0 * kvrow : nullptr;
     a.gate = gate ? static_cast<const uint16_t*>(gate) + (size_t)i0 * qrow : nullptr;
@@ -1179,13 +1195,18 @@ static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int
 // first one is made.  Launches of one call run in stream order and share the
 // workspace.
 static int decode_impl(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q,
-                       const void* k_new, const void* v_new, const void* gate, void* out, int32_t out_dtype,
-                       float scale, void* stream, float* part, uint32_t part_bytes, int32_t* counters,
-                       int64_t max_items, const char* workspace) {
+                       const void* k_new, const void* v_new, const void* gate, const DecodeProducer& prod,
+                       void* out, int32_t out_dtype, float scale, void* stream, float* part, uint32_t part_bytes,
+                       int32_t* counters, int64_t max_items, const char* workspace) {
     if (!c) return set_err(KVC_ERR_INVALID, "null context");
     int rc;
     if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
-    if (!q || !out) return set_err(KVC_ERR_INVALID, "decode needs q and out");
+    if (prod.qkv) {
+        if (!prod.q_norm || !prod.k_norm) return set_err(KVC_ERR_INVALID, "decode step needs q_norm and k_norm");
+    } else if (!q) {
+        return set_err(KVC_ERR_INVALID, "decode needs q and out");
+    }
+    if (!out) return set_err(KVC_ERR_INVALID, "decode needs q and out");
     if ((k_new == nullptr) != (v_new == nullptr)) return set_err(KVC_ERR_INVALID, "k_new and v_new go together");
     if (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16) return set_err(KVC_ERR_INVALID, "bad out_dtype");
     if (!std::isfinite(scale)) return set_err(KVC_ERR_INVALID, "scale must be finite");
@@ -1194,8 +1215,8 @@ static int decode_impl(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n
     for (int pass = 0; pass < 2; pass++) {
         for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
             const int32_t n = std::min(kMaxBatch, n_seqs - i0);
-            if ((rc = build_decode_args(c, layer, seqs, i0, n, q, k_new, v_new, gate, out, out_dtype, scale, part,
-                                        part_bytes, counters, max_items, workspace, a)))
+            if ((rc = build_decode_args(c, layer, seqs, i0, n, q, k_new, v_new, gate, prod, out, out_dtype, scale,
+                                        part, part_bytes, counters, max_items, workspace, a)))
                 return rc;
             if (pass == 1) {
                 int e = launch_decode(a, stream);
@@ -1208,16 +1229,29 @@ static int decode_impl(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n
 
 int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q, const void* k_new,
                     const void* v_new, const void* gate, void* out, int32_t out_dtype, float scale, void* stream) {
-    return decode_impl(c, layer, seqs, n_seqs, q, k_new, v_new, gate, out, out_dtype, scale, stream,
-                       c ? c->d_part : nullptr, (uint32_t)kPartBytes, c ? c->d_counters : nullptr,
+    return decode_impl(c, layer, seqs, n_seqs, q, k_new, v_new, gate, DecodeProducer{}, out, out_dtype, scale,
+                       stream, c ? c->d_part : nullptr, (uint32_t)kPartBytes, c ? c->d_counters : nullptr,
+                       (int64_t)kMaxChunks * kKvHeads, "context's split-K workspace");
+}
+
+int kvc_decode_step(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* qkv,
+                    const void* q_norm, const void* k_norm, void* out, int32_t out_dtype, float scale,
+                    void* stream) {
+    if (!qkv) return set_err(KVC_ERR_INVALID, "decode step needs qkv");
+    DecodeProducer prod;
+    prod.qkv = qkv;
+    prod.q_norm = q_norm;
+    prod.k_norm = k_norm;
+    return decode_impl(c, layer, seqs, n_seqs, nullptr, nullptr, nullptr, nullptr, prod, out, out_dtype, scale,
+                       stream, c ? c->d_part : nullptr, (uint32_t)kPartBytes, c ? c->d_counters : nullptr,
                        (int64_t)kMaxChunks * kKvHeads, "context's split-K workspace");
 }
 
 int kvc_decode_attn_static(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* q,
                            const void* k_new, const void* v_new, const void* gate, void* out, int32_t out_dtype,
                            float scale, void* stream) {
-    return decode_impl(c, layer, seqs, n_seqs, q, k_new, v_new, gate, out, out_dtype, scale, stream,
-                       c ? c->s_part : nullptr, (uint32_t)kStaticPartBytes, c ? c->s_counters : nullptr,
+    return decode_impl(c, layer, seqs, n_seqs, q, k_new, v_new, gate, DecodeProducer{}, out, out_dtype, scale,
+                       stream, c ? c->s_part : nullptr, (uint32_t)kStaticPartBytes, c ? c->s_counters : nullptr,
                        kStaticItems, "static decode workspace");
 }
 

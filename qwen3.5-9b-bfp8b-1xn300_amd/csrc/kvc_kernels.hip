@@ -375,14 +375,18 @@ __device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpoo
 // register buffers (the wait before each compute covers exactly the buffer it
 // reads while the other stays in flight); a window's last 1-3 blocks take a
 // straight-line tail of their own, so no load is ever issued for a block that
-// is not computed.
-template <int NP>
+// is not computed.  With PREP, prep() runs once, after the first blocks' loads
+// are issued and before anything uses qv (alone when there is no block): the
+// producing decode step builds qv there, so its arithmetic overlaps the first
+// loads.  That first group is peeled off the loop, so whatever prep() reads
+// is dead for the rest of the walk.
+template <int NP, bool PREP, typename Prep>
 __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
                                             const uint16_t* __restrict__ vpool,
                                             const int32_t* __restrict__ trow, int h, int blk0,
                                             int n_blk, int L, const uint32_t (&qv)[kGroup][2][4],
                                             float scale_log2, uint16_t* lds_p, WaveState& st,
-                                            int wave, int lane, int dpart) {
+                                            int wave, int lane, int dpart, Prep&& prep) {
     BlockRegs<NP> r0, r1;
     constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
 #define KVC_LOAD_WIN(R, I)                                                                          \
@@ -392,41 +396,209 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
     }
 #define KVC_NV(I) min(kBlockTok, L - (blk0 + w0 + (I)) * kBlockTok)
 #define KVC_COMPUTE(R, I) compute_block<NP>(R, qv, KVC_NV(I), scale_log2, lds_p, st, wave, lane)
-    for (int w0 = 0; w0 < n_blk; w0 += 64) {
+// blocks [i, wn) of the window at w0: groups of 4, then a tail of 1-3
+#define KVC_GROUPS                                  \
+    for (; i + 4 <= wn; i += 4) {                   \
+        KVC_LOAD_WIN(r0, i)                         \
+        KVC_LOAD_WIN(r1, i + 1)                     \
+        KVC_COMPUTE(r0, i);                         \
+        KVC_LOAD_WIN(r0, i + 2)                     \
+        KVC_COMPUTE(r1, i + 1);                     \
+        KVC_LOAD_WIN(r1, i + 3)                     \
+        KVC_COMPUTE(r0, i + 2);                     \
+        KVC_COMPUTE(r1, i + 3);                     \
+    }                                               \
+    {                                               \
+        const int rem = wn - i;                     \
+        if (rem == 1) {                             \
+            KVC_LOAD_WIN(r0, i)                     \
+            KVC_COMPUTE(r0, i);                     \
+        } else if (rem == 2) {                      \
+            KVC_LOAD_WIN(r0, i)                     \
+            KVC_LOAD_WIN(r1, i + 1)                 \
+            KVC_COMPUTE(r0, i);                     \
+            KVC_COMPUTE(r1, i + 1);                 \
+        } else if (rem == 3) {                      \
+            KVC_LOAD_WIN(r0, i)                     \
+            KVC_LOAD_WIN(r1, i + 1)                 \
+            KVC_COMPUTE(r0, i);                     \
+            KVC_LOAD_WIN(r0, i + 2)                 \
+            KVC_COMPUTE(r1, i + 1);                 \
+            KVC_COMPUTE(r0, i + 2);                 \
+        }                                           \
+    }
+    int wbeg = 0;
+    if constexpr (PREP) {
+        const int w0 = 0;
+        const int wn = min(64, n_blk);
+        const int my_id = lane < wn ? trow[blk0 + lane] : 0;
+        if (wn >= 4) {
+            KVC_LOAD_WIN(r0, 0)
+            KVC_LOAD_WIN(r1, 1)
+            prep();
+            KVC_COMPUTE(r0, 0);
+            KVC_LOAD_WIN(r0, 2)
+            KVC_COMPUTE(r1, 1);
+            KVC_LOAD_WIN(r1, 3)
+            KVC_COMPUTE(r0, 2);
+            KVC_COMPUTE(r1, 3);
+            int i = 4;
+            KVC_GROUPS
+        } else if (wn == 3) {
+            KVC_LOAD_WIN(r0, 0)
+            KVC_LOAD_WIN(r1, 1)
+            prep();
+            KVC_COMPUTE(r0, 0);
+            KVC_LOAD_WIN(r0, 2)
+            KVC_COMPUTE(r1, 1);
+            KVC_COMPUTE(r0, 2);
+        } else if (wn == 2) {
+            KVC_LOAD_WIN(r0, 0)
+            KVC_LOAD_WIN(r1, 1)
+            prep();
+            KVC_COMPUTE(r0, 0);
+            KVC_COMPUTE(r1, 1);
+        } else if (wn == 1) {
+            KVC_LOAD_WIN(r0, 0)
+            prep();
+            KVC_COMPUTE(r0, 0);
+        } else {
+            prep();
+        }
+        wbeg = 64;
+    }
+    for (int w0 = wbeg; w0 < n_blk; w0 += 64) {
         const int wn = min(64, n_blk - w0);
         const int my_id = lane < wn ? trow[blk0 + w0 + lane] : 0;
         int i = 0;
-        for (; i + 4 <= wn; i += 4) {
-            KVC_LOAD_WIN(r0, i)
-            KVC_LOAD_WIN(r1, i + 1)
-            KVC_COMPUTE(r0, i);
-            KVC_LOAD_WIN(r0, i + 2)
-            KVC_COMPUTE(r1, i + 1);
-            KVC_LOAD_WIN(r1, i + 3)
-            KVC_COMPUTE(r0, i + 2);
-            KVC_COMPUTE(r1, i + 3);
-        }
-        const int rem = wn - i;
-        if (rem == 1) {
-            KVC_LOAD_WIN(r0, i)
-            KVC_COMPUTE(r0, i);
-        } else if (rem == 2) {
-            KVC_LOAD_WIN(r0, i)
-            KVC_LOAD_WIN(r1, i + 1)
-            KVC_COMPUTE(r0, i);
-            KVC_COMPUTE(r1, i + 1);
-        } else if (rem == 3) {
-            KVC_LOAD_WIN(r0, i)
-            KVC_LOAD_WIN(r1, i + 1)
-            KVC_COMPUTE(r0, i);
-            KVC_LOAD_WIN(r0, i + 2)
-            KVC_COMPUTE(r1, i + 1);
-            KVC_COMPUTE(r0, i + 2);
-        }
+        KVC_GROUPS
     }
+#undef KVC_GROUPS
 #undef KVC_COMPUTE
 #undef KVC_NV
 #undef KVC_LOAD_WIN
+}
+
+// ---------------------------------------------------------------------------
+// Row arithmetic of the attention producer (per-head RMSNorm + partial RoPE),
+// shared by qkv_append_kernel and the producing decode step so both give the
+// same bits.  A row is held by a 32-lane half-wave, 8 dims per lane.
+template <bool BF16IN>
+__device__ __forceinline__ void load_row8(const void* base, size_t off, float (&x)[8]) {
+    if constexpr (BF16IN) {
+        const u32x4 u = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[2 * j] = bf16lo(u[j]);
+            x[2 * j + 1] = bf16hi(u[j]);
+        }
+    } else {
+        const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + off);
+        const u32x4 f0 = src[0];
+        const u32x4 f1 = src[1];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[j] = __uint_as_float(f0[j]);
+            x[4 + j] = __uint_as_float(f1[j]);
+        }
+    }
+}
+
+// RNE to bf16 with v_cvt_pk_bf16_f32 (a NaN input stays a NaN)
+__device__ __forceinline__ u32x4 pack_bf16x8(const float (&y)[8]) {
+    u32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; j++) w[j] = cvt_pk_bf16(y[2 * j], y[2 * j + 1]);
+    return w;
+}
+__device__ __forceinline__ void store_bf16x8(uint16_t* dst, const float (&y)[8]) {
+    __builtin_nontemporal_store(pack_bf16x8(y), reinterpret_cast<u32x4*>(dst));
+}
+
+// yp = y of lane ^ M (M < 32: ds_swizzle, no address arithmetic)
+template <int M>
+__device__ __forceinline__ void swap_lanes8(const float (&y)[8], float (&yp)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) yp[j] = shfl_xor<M>(y[j]);
+}
+
+// sum over the 32 lanes of each wave half
+__device__ __forceinline__ float half_wave_sum(float x) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    x += dpp<kDppRowRor8>(x);
+    return sum_xor16(x);
+}
+
+// RoPE coefficients of the 8 dims d0 .. d0+7 of a lane at position pos:
+// table entries p0 .. p0+7 for rope_dim >= 16, entries 0..3 twice for
+// rope_dim 8; cos 1 / sin 0 outside the rotated dims or with no RoPE.
+__device__ __forceinline__ void load_rope8(const float* rope, int rope_rows, int half, int pos, int d0,
+                                           float (&cs)[8], float (&sn)[8]) {
+    if (d0 < 2 * half) {
+        const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
+        const float* crow = rope + (size_t)pos * half + p0;
+        const float* srow = rope + ((size_t)rope_rows + pos) * half + p0;
+        const float4 c0 = *reinterpret_cast<const float4*>(crow);
+        const float4 s0 = *reinterpret_cast<const float4*>(srow);
+        const float4 c1 = half >= 8 ? *reinterpret_cast<const float4*>(crow + 4) : c0;
+        const float4 s1 = half >= 8 ? *reinterpret_cast<const float4*>(srow + 4) : s0;
+        cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w;
+        cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
+        sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            cs[j] = 1.f;
+            sn[j] = 0.f;
+        }
+    }
+}
+
+// One head row held by a 32-lane half-wave, 8 dims per lane (d0 = 8 x lane
+// in the half): per-head RMSNorm with weights wn, then partial NeoX RoPE
+// (partner of dim p < half is p + half: lane ^ (half / 8), or inside the
+// lane for rope_dim 8), in the reference's order (src/engine.cpp:3497-3512):
+// (x * r) * w, then x0 c - x1 s and x1 c + x0 s, without contraction.  Both
+// the producer kernel and the fused decode step use it, so they give the same
+// bits.
+__device__ __forceinline__ void norm_rope_row8(const float (&x)[8], const float (&wn)[8], float eps, int half,
+                                               int d0, const float (&cs)[8], const float (&sn)[8], float (&y)[8]) {
+#pragma clang fp contract(off)
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) ss += x[j] * x[j];
+    ss = half_wave_sum(ss);
+    const float rs = 1.0f / sqrtf(ss / kHeadDim + eps);
+#pragma unroll
+    for (int j = 0; j < 8; j++) y[j] = x[j] * rs * wn[j];
+    const bool roped = d0 < 2 * half;
+    if (half >= 8) {
+        float yp[8];
+        switch (half) {  // partner lane ^ (half / 8), uniform
+            case 8: swap_lanes8<1>(y, yp); break;
+            case 16: swap_lanes8<2>(y, yp); break;
+            case 32: swap_lanes8<4>(y, yp); break;
+            case 64: swap_lanes8<8>(y, yp); break;
+            default: swap_lanes8<16>(y, yp); break;
+        }
+        if (roped) {
+            const bool low = d0 < half;
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[j] = low ? y[j] * cs[j] - yp[j] * sn[j] : y[j] * cs[j] + yp[j] * sn[j];
+        }
+    } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
+        float z[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            z[j] = y[j] * cs[j] - y[j + 4] * sn[j];
+            z[j + 4] = y[j + 4] * cs[j + 4] + y[j] * sn[j + 4];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) y[j] = z[j];
+    }
 }
 
 // Fold one extra key (the fused-append token, bf16 rows knew/vnew of this kv
@@ -559,7 +731,18 @@ __device__ __forceinline__ void combine_batch(__amdgpu_buffer_rsrc_t prs, int it
     }
 }
 
-template <int NP>
+// PRODUCE: the decode step with the attention producer fused in (one query
+// token per sequence, bf16 projection rows a.qkv).  Each wave builds the 4 q
+// rows of its group itself, 2 rows at a time (one per 32-lane half), with the
+// producer's own row arithmetic (norm_rope_row8: per-head RMSNorm + partial
+// RoPE at position L - 1, RNE bf16), stages them in its own slice of sm.acc
+// and reads them back in load_q's layout: no workgroup barrier.  The raw rows,
+// norm weights and RoPE coefficients are requested before the block walk and
+// the arithmetic runs after the walk's first loads are issued (prep).  Wave 0
+// of the workgroup that owns the new position also builds its k row (and
+// stages the raw v row); the fused-append path then folds and appends them
+// from LDS.  The gate is read straight from the projection row.
+template <int NP, bool PRODUCE>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     __shared__ DecodeSmem sm;
     KVC_STAMP(0);
@@ -582,21 +765,87 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int new_pos = a.k_new ? L - 1 : -1;
-    const uint16_t* knew = a.k_new ? a.k_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
-    const uint16_t* vnew = a.v_new ? a.v_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
+    const bool fused_new = PRODUCE || a.k_new != nullptr;
+    const int new_pos = fused_new ? L - 1 : -1;
+    // PRODUCE: wave w's staging rows in LDS (q heads 0..3 of the group, then
+    // k and v of the new token in wave 0); sm.acc is next written by the merge
+    uint16_t* const stage = reinterpret_cast<uint16_t*>(&sm.acc[wave][0][0]);
+    const uint16_t* knew;
+    const uint16_t* vnew;
+    if constexpr (PRODUCE) {
+        knew = reinterpret_cast<const uint16_t*>(&sm.acc[0][0][0]) + kGroup * kHeadDim;
+        vnew = knew + kHeadDim;
+    } else {
+        knew = a.k_new ? a.k_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
+        vnew = a.v_new ? a.v_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
+    }
 
     uint32_t qv[kGroup][2][4];
-    load_q(qv, a.q + ((size_t)s * kQHeads + h * kGroup) * kHeadDim, lane);
+    // PRODUCE inputs, held from here to prep: lane hl = lane % 32 of half
+    // sub = lane / 32 has dims pd0 .. pd0 + 7 of q rows 2i + sub (raw bf16),
+    // of the k (sub 0) or v (sub 1) row of the new token (owner's wave 0),
+    // their norm weights and the RoPE coefficients of position L - 1
+    const int sub = lane >> 5, pd0 = (lane & 31) * 8;
+    const bool make_new = PRODUCE && wave == 0 && new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
+    u32x4 xq[2], xkv;
+    float wq[8], wk[8], cs[8], sn[8];
+    if constexpr (PRODUCE) {
+        const uint16_t* prow = a.qkv + (size_t)s * kQkvRow;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            xq[i] = *reinterpret_cast<const u32x4*>(prow + (size_t)(h * kGroup + 2 * i + sub) * 2 * kHeadDim + pd0);
+        const float4 w0 = *reinterpret_cast<const float4*>(a.q_norm + pd0);
+        const float4 w1 = *reinterpret_cast<const float4*>(a.q_norm + pd0 + 4);
+        wq[0] = w0.x; wq[1] = w0.y; wq[2] = w0.z; wq[3] = w0.w;
+        wq[4] = w1.x; wq[5] = w1.y; wq[6] = w1.z; wq[7] = w1.w;
+        if (make_new) {
+            constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
+            xkv = *reinterpret_cast<const u32x4*>(prow + kKOff + (size_t)(sub * kKvHeads + h) * kHeadDim + pd0);
+            const float4 k0 = *reinterpret_cast<const float4*>(a.k_norm + pd0);
+            const float4 k1 = *reinterpret_cast<const float4*>(a.k_norm + pd0 + 4);
+            wk[0] = k0.x; wk[1] = k0.y; wk[2] = k0.z; wk[3] = k0.w;
+            wk[4] = k1.x; wk[5] = k1.y; wk[6] = k1.z; wk[7] = k1.w;
+        }
+        load_rope8(a.rope, a.rope_rows, a.rope_half, new_pos, pd0, cs, sn);
+    } else {
+        load_q(qv, a.q + ((size_t)s * kQHeads + h * kGroup) * kHeadDim, lane);
+    }
+    auto prep = [&]() {
+        if constexpr (PRODUCE) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                float x[8], y[8];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    x[2 * j] = bf16lo(xq[i][j]);
+                    x[2 * j + 1] = bf16hi(xq[i][j]);
+                }
+                norm_rope_row8(x, wq, a.eps, a.rope_half, pd0, cs, sn, y);
+                *reinterpret_cast<u32x4*>(stage + (2 * i + sub) * kHeadDim + pd0) = pack_bf16x8(y);
+            }
+            if (make_new) {  // uniform
+                float x[8], y[8];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    x[2 * j] = bf16lo(xkv[j]);
+                    x[2 * j + 1] = bf16hi(xkv[j]);
+                }
+                norm_rope_row8(x, wk, a.eps, a.rope_half, pd0, cs, sn, y);  // half 1 (v): unused
+                *reinterpret_cast<u32x4*>(stage + (kGroup + sub) * kHeadDim + pd0) = sub ? xkv : pack_bf16x8(y);
+            }
+            wave_lds_sync();
+            load_q(qv, stage, lane);
+        }
+    };
     WaveState st;
     init_state(st);
     // keys [0, Lw) come from the pool; with a fused append the last key
     // (position L-1) comes from knew/vnew and is folded in by wave 0 of the
     // chunk that owns it, whose part 0 also writes it into the pool
-    const int Lw = a.k_new ? L - 1 : L;
+    const int Lw = fused_new ? L - 1 : L;
     const int wblk1 = min(blk1, (Lw + kBlockTok - 1) / kBlockTok);
-    walk_blocks<NP>(a.kpool, a.vpool, trow, h, blk0, max(0, wblk1 - blk0), Lw, qv, a.scale_log2, sm.p16[wave],
-                    st, wave, lane, dpart);
+    walk_blocks<NP, PRODUCE>(a.kpool, a.vpool, trow, h, blk0, max(0, wblk1 - blk0), Lw, qv, a.scale_log2,
+                             sm.p16[wave], st, wave, lane, dpart, prep);
     finalize_l(st);
     const bool owns_new = new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
     if (owns_new) {
@@ -657,10 +906,13 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     }
     KVC_STAMP(2);
     const size_t orow = ((size_t)s * kQHeads + h * kGroup + g) * kHeadDim;
-    const bool has_gate = a.gate != nullptr;
+    const bool has_gate = PRODUCE || a.gate != nullptr;
+    // gate row of q head h * kGroup + g: its own tensor, or the projection row
+    const uint16_t* grow = PRODUCE ? a.qkv + (size_t)s * kQkvRow + (size_t)(h * kGroup + g) * 2 * kHeadDim + kHeadDim
+                                   : a.gate + orow;
     uint2 gw = make_uint2(0u, 0u);  // gate words of this thread's dims
     if (n_chunks == 1) {
-        if (has_gate && act) gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+        if (has_gate && act) gw = *reinterpret_cast<const uint2*>(grow + d0);
         if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lsum, A);
 #ifdef KVC_PHASE_STAMPS
         __builtin_amdgcn_s_waitcnt(0);
@@ -702,7 +954,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     // arrive while it completes, so a combiner does not wait on them after
     // its fold and no wave waits on them before its arrival
     asm volatile("" ::: "memory");
-    if (has_gate && act) gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+    if (has_gate && act) gw = *reinterpret_cast<const uint2*>(grow + d0);
     const bool last = __builtin_amdgcn_readfirstlane(prev) == n_chunks - 1;
     KVC_STAMP(4);
     if (!last) return;
@@ -1271,51 +1523,6 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
 // 57.7 us, against 61.0 us with non-temporal loads).
 constexpr int kQkvWaves = 5;
 
-template <bool BF16IN>
-__device__ __forceinline__ void load_row8(const void* base, size_t off, float (&x)[8]) {
-    if constexpr (BF16IN) {
-        const u32x4 u = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(base) + off);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            x[2 * j] = bf16lo(u[j]);
-            x[2 * j + 1] = bf16hi(u[j]);
-        }
-    } else {
-        const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + off);
-        const u32x4 f0 = src[0];
-        const u32x4 f1 = src[1];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            x[j] = __uint_as_float(f0[j]);
-            x[4 + j] = __uint_as_float(f1[j]);
-        }
-    }
-}
-
-// RNE to bf16 with v_cvt_pk_bf16_f32 (a NaN input stays a NaN)
-__device__ __forceinline__ void store_bf16x8(uint16_t* dst, const float (&y)[8]) {
-    u32x4 w;
-#pragma unroll
-    for (int j = 0; j < 4; j++) w[j] = cvt_pk_bf16(y[2 * j], y[2 * j + 1]);
-    __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(dst));
-}
-
-// yp = y of lane ^ M (M < 32: ds_swizzle, no address arithmetic)
-template <int M>
-__device__ __forceinline__ void swap_lanes8(const float (&y)[8], float (&yp)[8]) {
-#pragma unroll
-    for (int j = 0; j < 8; j++) yp[j] = shfl_xor<M>(y[j]);
-}
-
-// sum over the 32 lanes of each wave half
-__device__ __forceinline__ float half_wave_sum(float x) {
-    x += dpp<kDppXor1>(x);
-    x += dpp<kDppXor2>(x);
-    x += dpp<kDppHalfMirror>(x);
-    x += dpp<kDppRowRor8>(x);
-    return sum_xor16(x);
-}
-
 // tokens per producer workgroup (all their rows are loaded first); 2 and 4
 // tokens measured no faster than 1
 constexpr int kQkvTok = 1;
@@ -1331,7 +1538,6 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
     const bool kv_wave = wave == kQkvWaves - 1;  // rows 16..19: the kv heads
     constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
     const int half = a.rope_half;
-    const bool roped = d0 < 2 * half;
     const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
 
     // every input row of this lane, for every token of the workgroup, is
@@ -1360,28 +1566,7 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
                     load_row8<BF16IN>(a.qkv, co + d0, c[tt][i]);
             }
         }
-        // RoPE coefficients of this lane's 8 dims: table entries p0 .. p0+7
-        // for rope_dim >= 16, entries 0..3 twice for rope_dim 8
-        const int pos = a.pos0[s] + tok;
-        if (roped) {
-            const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
-            const float* crow = a.rope + (size_t)pos * half + p0;
-            const float* srow = a.rope + ((size_t)a.rope_rows + pos) * half + p0;
-            const float4 c0 = *reinterpret_cast<const float4*>(crow);
-            const float4 s0 = *reinterpret_cast<const float4*>(srow);
-            const float4 c1 = half >= 8 ? *reinterpret_cast<const float4*>(crow + 4) : c0;
-            const float4 s1 = half >= 8 ? *reinterpret_cast<const float4*>(srow + 4) : s0;
-            cs[tt][0] = c0.x; cs[tt][1] = c0.y; cs[tt][2] = c0.z; cs[tt][3] = c0.w;
-            cs[tt][4] = c1.x; cs[tt][5] = c1.y; cs[tt][6] = c1.z; cs[tt][7] = c1.w;
-            sn[tt][0] = s0.x; sn[tt][1] = s0.y; sn[tt][2] = s0.z; sn[tt][3] = s0.w;
-            sn[tt][4] = s1.x; sn[tt][5] = s1.y; sn[tt][6] = s1.z; sn[tt][7] = s1.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                cs[tt][j] = 1.f;
-                sn[tt][j] = 0.f;
-            }
-        }
+        load_rope8(a.rope, a.rope_rows, half, a.pos0[s] + tok, d0, cs[tt], sn[tt]);
     }
     const float* wrow = (kv_wave ? a.k_norm : a.q_norm) + d0;
     const float4 w0 = *reinterpret_cast<const float4*>(wrow);
@@ -1418,39 +1603,8 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int r = wave * 4 + i * 2 + sub;  // 0..15 q heads, 16..19 k heads
-            float ss = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) ss += x[tt][i][j] * x[tt][i][j];
-            ss = half_wave_sum(ss);
-            const float rs = 1.0f / sqrtf(ss / kHeadDim + a.eps);
             float y[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) y[j] = x[tt][i][j] * rs * wn[j];
-            if (half >= 8) {
-                float yp[8];
-                switch (half) {  // partner lane ^ (half / 8), uniform
-                    case 8: swap_lanes8<1>(y, yp); break;
-                    case 16: swap_lanes8<2>(y, yp); break;
-                    case 32: swap_lanes8<4>(y, yp); break;
-                    case 64: swap_lanes8<8>(y, yp); break;
-                    default: swap_lanes8<16>(y, yp); break;
-                }
-                if (roped) {
-                    const bool low = d0 < half;
-#pragma unroll
-                    for (int j = 0; j < 8; j++)
-                        y[j] = low ? y[j] * cs[tt][j] - yp[j] * sn[tt][j] : y[j] * cs[tt][j] + yp[j] * sn[tt][j];
-                }
-            } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
-                float z[8];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    z[j] = y[j] * cs[tt][j] - y[j + 4] * sn[tt][j];
-                    z[j + 4] = y[j + 4] * cs[tt][j + 4] + y[j] * sn[tt][j + 4];
-                }
-#pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = z[j];
-            }
+            norm_rope_row8(x[tt][i], wn, a.eps, half, d0, cs[tt], sn[tt], y);
             if (kv_wave) {
                 const size_t slot =
                     (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
@@ -2668,10 +2822,17 @@ int static_scratch(int device, float** part, int32_t** counters) {
 
 int launch_decode(const DecodeArgs& a, void* stream) {
     const int grid = a.per_xcd * 8;
-    if (a.d_parts == 2)
-        hipLaunchKernelGGL(decode_kernel<2>, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
-    else
-        hipLaunchKernelGGL(decode_kernel<1>, dim3(grid), dim3(kWaves * 64), 0, (hipStream_t)stream, a);
+    const hipStream_t st = (hipStream_t)stream;
+    if (a.qkv) {
+        if (a.d_parts == 2)
+            hipLaunchKernelGGL((decode_kernel<2, true>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+        else
+            hipLaunchKernelGGL((decode_kernel<1, true>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+    } else if (a.d_parts == 2) {
+        hipLaunchKernelGGL((decode_kernel<2, false>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+    } else {
+        hipLaunchKernelGGL((decode_kernel<1, false>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+    }
     return (int)hipGetLastError();
 }
 

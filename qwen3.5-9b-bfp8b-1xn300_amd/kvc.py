@@ -43,7 +43,7 @@ EXPORTS = [
     "kvc_get_stats", "kvc_abi_version", "kvc_seq_create", "kvc_seq_release",
     "kvc_seq_reset", "kvc_seq_len", "kvc_seq_truncate", "kvc_seq_reserve",
     "kvc_seq_commit", "kvc_prefix_match", "kvc_append", "kvc_qkv_append", "kvc_decode_attn",
-    "kvc_decode_attn_static", "kvc_prefill_attn", "kvc_gather", "kvc_kv_checksum", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
+    "kvc_decode_attn_static", "kvc_decode_step", "kvc_prefill_attn", "kvc_gather", "kvc_kv_checksum", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
     "kvc_snapshot_restore", "kvc_snapshot_release", "kvc_pool_fill_normal",
     "kvc_fill_normal_bf16", "kvc_sync",
 ]
@@ -114,6 +114,7 @@ def lib() -> ctypes.CDLL:
             "kvc_qkv_append": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, P, P]),
             "kvc_decode_attn": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
             "kvc_decode_attn_static": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
+            "kvc_decode_step": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, I32, F32, P]),
             "kvc_kv_checksum": (ctypes.c_int, [P, I32, pI32, I32, P, P]),
             "kvc_prefill_attn": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P, I32, F32, P]),
             "kvc_gather": (ctypes.c_int, [P, I32, pI32, I32, I32, pI32, P, P, P]),
@@ -386,6 +387,12 @@ class Context:
         _check(self.L.kvc_decode_attn_static(self.ptr, layer, _i32(seqs), len(seqs), self._p(q), self._p(k_new),
                                              self._p(v_new), self._p(gate), self._p(out), out_dtype,
                                              ctypes.c_float(scale), stream))
+
+    def decode_step(self, layer, seqs, qkv, q_norm, k_norm, out, out_dtype=DTYPE_F32, scale=1.0 / 16,
+                    stream=None):
+        """qkv_append (bf16 rows, one token) + gated decode_attn in one launch"""
+        _check(self.L.kvc_decode_step(self.ptr, layer, _i32(seqs), len(seqs), self._p(qkv), self._p(q_norm),
+                                      self._p(k_norm), self._p(out), out_dtype, ctypes.c_float(scale), stream))
 
     def prefill_attn(self, layer, seqs, n_q, q, out, gate=None, out_dtype=DTYPE_F32,
                      scale=1.0 / 16, stream=None):
