@@ -42,6 +42,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 NQ, NKV, D, BT = 16, 4, 256, 32
 ROW = NKV * D
+QKV_ROW = NQ * 2 * D + 2 * ROW  # attention projection row: [Hq][q | gate][D], k, v
 SEED = 20261201
 O_SSM_PROJ = 8192 + 4096 + 2 * 32  # Gated-DeltaNet projection row: conv inputs, z, alpha, beta
 DN_TOKEN_FLOP = 32 * 128 * 128 * 7  # delta rule, one token and layer: 7 flop per recurrent-state element
@@ -137,10 +138,20 @@ class DecodeB:
     Python host loop ahead of the GPU.  tests/test_gpu_bench_b.py checks
     these launches against the oracle."""
 
-    def __init__(self, reps=4, chunk_blocks=0, L=4096, layers=8):
+    STEP_MODES = ("decode", "two_launch", "fused")
+
+    def __init__(self, reps=4, chunk_blocks=0, L=4096, layers=8, mode="decode"):
+        """mode "decode": the headline launch above (q, gate, k/v rows given).
+        The whole attention step from the projection row (q/k RMSNorm +
+        partial RoPE, k/v append, gated decode): "two_launch" =
+        kvc_qkv_append then kvc_decode_attn on its q and gate (walking the
+        appended key), "fused" = kvc_decode_step (one launch)."""
         import kvc
 
+        if mode not in self.STEP_MODES:
+            raise ValueError(f"mode must be one of {self.STEP_MODES}")
         self.kvc = kvc
+        self.mode = mode
         h = self.h = kvc.hip()
         if h.device_count() < 1:
             raise RuntimeError("no HIP device visible")
@@ -164,6 +175,13 @@ class DecodeB:
         ctx.fill_normal_bf16(self.kn, n * ROW, SEED + 5, 1.0, stream)
         ctx.fill_normal_bf16(self.vn, n * ROW, SEED + 6, 1.0, stream)
         ctx.fill_normal_bf16(self.gate, n * NQ * D, SEED + 7, 1.0, stream)
+        # projection rows [Hq][q | gate][D], k [Hkv][D], v [Hkv][D] and the
+        # q / k norm weights of the step modes
+        self.qkv = h.malloc(n * QKV_ROW * 2)
+        ctx.fill_normal_bf16(self.qkv, n * QKV_ROW, SEED + 8, 1.0, stream)
+        rng = np.random.default_rng(SEED + 9)
+        self.q_norm = h.malloc(D * 4).upload(rng.uniform(0.5, 1.5, D).astype(np.float32))
+        self.k_norm = h.malloc(D * 4).upload(rng.uniform(0.5, 1.5, D).astype(np.float32))
         h.stream_sync(stream)
         ctx.reserve(seqs, 1, stream)
         self.graph = h.capture(stream, lambda: [self.enqueue_step(r) for r in range(reps)])
@@ -176,12 +194,38 @@ class DecodeB:
             ctx.seq_truncate(s_, L - 1)
 
     def enqueue_step(self, r):
+        bf16 = self.kvc.DTYPE_BF16
         for layer in range(self.layers):
             i = r * self.layers + layer
-            self.ctx.decode_attn(layer, [self.seqs[r]], self.q.ptr + i * NQ * D * 2, self.out.ptr + i * NQ * D * 2,
-                                 k_new=self.kn.ptr + i * ROW * 2, v_new=self.vn.ptr + i * ROW * 2,
-                                 gate=self.gate.ptr + i * NQ * D * 2, out_dtype=self.kvc.DTYPE_BF16,
-                                 scale=1.0 / 16, stream=self.stream)
+            seq = [self.seqs[r]]
+            q, out, gate = (b_.ptr + i * NQ * D * 2 for b_ in (self.q, self.out, self.gate))
+            if self.mode == "decode":
+                self.ctx.decode_attn(layer, seq, q, out, k_new=self.kn.ptr + i * ROW * 2,
+                                     v_new=self.vn.ptr + i * ROW * 2, gate=gate, out_dtype=bf16,
+                                     scale=1.0 / 16, stream=self.stream)
+                continue
+            qkv = self.qkv.ptr + i * QKV_ROW * 2
+            if self.mode == "two_launch":
+                self.ctx.qkv_append(layer, seq, 1, qkv, self.q_norm, self.k_norm, q_out=q, gate_out=gate,
+                                    in_dtype=bf16, stream=self.stream)
+                self.ctx.decode_attn(layer, seq, q, out, gate=gate, out_dtype=bf16, scale=1.0 / 16,
+                                     stream=self.stream)
+            else:
+                self.ctx.decode_step(layer, seq, qkv, self.q_norm, self.k_norm, out, out_dtype=bf16,
+                                     scale=1.0 / 16, stream=self.stream)
+
+    def set_mode(self, mode):
+        """Re-capture the step graphs for another step mode."""
+        if mode not in self.STEP_MODES:
+            raise ValueError(f"mode must be one of {self.STEP_MODES}")
+        h, stream, reps = self.h, self.stream, self.reps
+        for g_ in [self.graph] + self.single:
+            h.graph_destroy(g_)
+        self.mode = mode
+        self.ctx.reserve(self.seqs, 1, stream)
+        self.graph = h.capture(stream, lambda: [self.enqueue_step(r) for r in range(reps)])
+        self.single = [h.capture(stream, lambda r=r: self.enqueue_step(r)) for r in range(reps)]
+        self.end_round()
 
     def enqueue_floor(self, r):
         per = (self.L // BT) * 2 * NKV
@@ -220,7 +264,7 @@ class DecodeB:
     def close(self):
         for g_ in [self.graph, self.floor_graph] + self.single:
             self.h.graph_destroy(g_)
-        for b_ in (self.q, self.kn, self.vn, self.out, self.gate, self.sums):
+        for b_ in (self.q, self.kn, self.vn, self.out, self.gate, self.sums, self.qkv, self.q_norm, self.k_norm):
             b_.free()
         self.ctx.close()
 
@@ -259,6 +303,16 @@ def run_b(args):
     B.run_floor(f_rounds)
     h.record(e1, stream)
     floor_us = h.elapsed_ms(e0, e1) * 1e3 / (f_rounds * B.reps * layers)
+    # the whole attention step from the projection row, two launches against one
+    step_us = {}
+    for mode in ("two_launch", "fused"):
+        B.set_mode(mode)
+        B.run_steps(args.warmup)
+        h.stream_sync(stream)
+        h.record(e0, stream)
+        B.run_steps(steps)
+        h.record(e1, stream)
+        step_us[mode] = h.elapsed_ms(e0, e1) * 1e3 / (steps * layers)
     B.close()
 
     line = {
@@ -285,6 +339,14 @@ def run_b(args):
         "floor_note": "one checksum_kernel launch reading the same 16 MiB of K/V (whole blocks) per layer, "
                       "same graph and replica rotation: the single-launch read floor",
         "pct_of_floor": round(100 * floor_us / us_layer, 1),
+        "attention_step": {
+            "two_launch_us_per_layer": round(step_us["two_launch"], 3),
+            "fused_us_per_layer": round(step_us["fused"], 3),
+            "note": "the whole attention step of a decode token from its bf16 projection row (q/k RMSNorm + "
+                    "partial RoPE, k/v append, gated decode) per layer, same graph setup: kvc_qkv_append + "
+                    "kvc_decode_attn (two launches; the decode walks the appended key) against "
+                    "kvc_decode_step (one launch; it folds the new key in after the walk, as "
+                    "kvc_decode_attn does with k_new / v_new, and matches that bit for bit)"},
         "host_wall_us_per_step": round(wall * 1e6 / steps, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),

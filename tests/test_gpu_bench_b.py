@@ -60,6 +60,48 @@ def test_headline_decode_launch_as_benched():
         B.close()
 
 
+def test_attention_step_modes_as_benched():
+    """bench.py's attention_step leg: the round graph of each step mode
+    (kvc_qkv_append + kvc_decode_attn, then kvc_decode_step) replayed after
+    warm-up.  Both append the same slots bit for bit.  Their outputs differ
+    only in where the newest key enters the softmax (walked from the pool
+    after the producer's append, or folded in after the walk by the fused
+    step), so each mode is checked against the oracle over the gathered keys
+    with the produced q and gate, and the two against each other within the
+    decode tolerance."""
+    say("bench config b: attention step, two launches against one")
+    B = bench.DecodeB(reps=4, mode="two_launch")
+    try:
+        h, L, layers, reps = B.h, B.L, B.layers, B.reps
+        n = reps * layers
+        got = {}
+        for mode in ("two_launch", "fused"):
+            if mode != B.mode:
+                B.set_mode(mode)
+            B.run_steps(2 * reps)
+            B.begin_round()
+            h.graph_launch(B.graph, B.stream)
+            h.stream_sync(B.stream)
+            out = B.out.download(np.uint16, (n, NQ, D))
+            slots = [gather(B.ctx, i % layers, [B.seqs[i // layers]], [1], tok0=L - 1)[0] for i in range(n)]
+            got[mode] = (out, slots)
+            if mode == "two_launch":  # the producer's q and gate (the fused step keeps them on chip)
+                q = B.q.download(np.uint16, (n, NQ, D))
+                gate = B.gate.download(np.uint16, (n, NQ, D))
+            for i in (0, n - 1):
+                (k, v), = gather(B.ctx, i % layers, [B.seqs[i // layers]], [L])
+                ref = O.decode_attn(q[i], k, v, L, gate=gate[i], gate_mode=1)
+                O.assert_attn_close(O.bf16_to_f32(out[i]), ref, what=f"{mode} step {i}")
+            B.end_round()
+        (o1, s1), (o2, s2) = got["two_launch"], got["fused"]
+        for i in range(n):
+            assert np.array_equal(s1[i][0], s2[i][0]) and np.array_equal(s1[i][1], s2[i][1]), f"slot {i}"
+            O.assert_attn_close(O.bf16_to_f32(o2[i]), O.bf16_to_f32(o1[i]).astype(np.float64),
+                                what=f"replica {i // layers} layer {i % layers}: fused vs two launches")
+    finally:
+        B.close()
+
+
 def test_phase_stamps_build_runs():
     """bench.py --config b --phases (the KVC_PHASE_STAMPS build,
     libkvc_phases.so) in a child process, since this one has libkvc.so
