@@ -932,7 +932,7 @@ def run_phases(args, launches=40):
     import ctypes
     import kvc
 
-    B = DecodeB(reps=args.replicas, chunk_blocks=args.chunk_blocks)
+    B = DecodeB(reps=args.replicas, chunk_blocks=args.chunk_blocks, mode=args.step_mode)
     h = B.h
     try:
         L = kvc.lib()
@@ -946,6 +946,8 @@ def run_phases(args, launches=40):
         h.stream_sync(B.stream)
         rows = {p: [] for p in PHASE_POINTS}
         crows = {p: [] for p in PHASE_POINTS}
+        prep_rows = []  # point 8: q rows built (producing decode step)
+        prep0_rows = []  # point 9: their arithmetic begins
         for it in range(launches):
             r = it % B.reps
             stamps.zero()
@@ -967,16 +969,27 @@ def run_phases(args, launches=40):
                     rows[p].append((us[:, :, i][sel].mean(), us[:, :, i][sel].max(), int(sel.sum())))
                 if comb.any():
                     crows[p].append((us[:, :, i][comb].mean(), us[:, :, i][comb].max(), int(comb.sum())))
+            if npt > len(PHASE_POINTS):
+                sel = live & (t[:, :, 8] >= t[:, :, 0])
+                if sel.any():
+                    prep_rows.append((us[:, :, 8][sel].mean(), us[:, :, 8][sel].max(), int(sel.sum())))
+                sel = live & (t[:, :, 9] >= t[:, :, 0])
+                if sel.any():
+                    prep0_rows.append((us[:, :, 9][sel].mean(), us[:, :, 9][sel].max(), int(sel.sum())))
     finally:
         B.close()
     def summary(rs):
         return {p: {"mean_us": round(float(np.mean([v[0] for v in rs[p]])), 2),
                     "max_us": round(float(np.mean([v[1] for v in rs[p]])), 2),
-                    "waves": int(round(np.mean([v[2] for v in rs[p]])))} for p in PHASE_POINTS if rs[p]}
+                    "waves": int(round(np.mean([v[2] for v in rs[p]])))} for p in rs if rs[p]}
 
-    return {"metric": "decode_kernel phase stamps, config b (libkvc_phases.so)", "launches": launches,
-            "unit": "us since the launch's first workgroup entered", "phases": summary(rows),
-            "combining_waves": summary(crows)}
+    res = {"metric": "decode_kernel phase stamps, config b (libkvc_phases.so)", "step_mode": args.step_mode,
+           "launches": launches,
+           "unit": "us since the launch's first workgroup entered", "phases": summary(rows),
+           "combining_waves": summary(crows)}
+    if prep_rows:
+        res["q_rows"] = summary({"arithmetic begins": prep0_rows, "built": prep_rows})
+    return res
 
 
 def main():
@@ -994,6 +1007,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--phases", action="store_true",
                     help="config b's decode launch with phase stamps (libkvc_phases.so); prints the phase table")
+    ap.add_argument("--step-mode", default="decode", choices=["decode", "two_launch", "fused"],
+                    help="with --phases: the step whose decode launch is stamped (bench.DecodeB modes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the KV path "

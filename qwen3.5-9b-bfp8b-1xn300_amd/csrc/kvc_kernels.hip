@@ -429,13 +429,22 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
     }
     int wbeg = 0;
     if constexpr (PREP) {
+        // first window: the loads of blocks 0 and 1 (those that exist), prep
+        // (inlined once: it runs once per launch, so its code stays small),
+        // then the first group or the whole short window
         const int w0 = 0;
         const int wn = min(64, n_blk);
         const int my_id = lane < wn ? trow[blk0 + lane] : 0;
+        // both block ids are read on every path, so every load issued before
+        // the table's (what prep consumes) is known complete past this point
+        // and prep waits on none of the block loads below
+        const int id0 = __builtin_amdgcn_readlane(my_id, 0), id1 = __builtin_amdgcn_readlane(my_id, 1);
+        if (wn >= 1) load_block<NP>(r0, kpool + ((size_t)id0 * kKvHeads + h) * kUnitElems,
+                                    vpool + ((size_t)id0 * kKvHeads + h) * kUnitElems, wave, lane, dpart);
+        if (wn >= 2) load_block<NP>(r1, kpool + ((size_t)id1 * kKvHeads + h) * kUnitElems,
+                                    vpool + ((size_t)id1 * kKvHeads + h) * kUnitElems, wave, lane, dpart);
+        prep();
         if (wn >= 4) {
-            KVC_LOAD_WIN(r0, 0)
-            KVC_LOAD_WIN(r1, 1)
-            prep();
             KVC_COMPUTE(r0, 0);
             KVC_LOAD_WIN(r0, 2)
             KVC_COMPUTE(r1, 1);
@@ -445,25 +454,15 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
             int i = 4;
             KVC_GROUPS
         } else if (wn == 3) {
-            KVC_LOAD_WIN(r0, 0)
-            KVC_LOAD_WIN(r1, 1)
-            prep();
             KVC_COMPUTE(r0, 0);
             KVC_LOAD_WIN(r0, 2)
             KVC_COMPUTE(r1, 1);
             KVC_COMPUTE(r0, 2);
         } else if (wn == 2) {
-            KVC_LOAD_WIN(r0, 0)
-            KVC_LOAD_WIN(r1, 1)
-            prep();
             KVC_COMPUTE(r0, 0);
             KVC_COMPUTE(r1, 1);
         } else if (wn == 1) {
-            KVC_LOAD_WIN(r0, 0)
-            prep();
             KVC_COMPUTE(r0, 0);
-        } else {
-            prep();
         }
         wbeg = 64;
     }
@@ -480,8 +479,8 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
 }
 
 // ---------------------------------------------------------------------------
-// Row arithmetic of the attention producer (per-head RMSNorm + partial RoPE),
-// shared by qkv_append_kernel and the producing decode step so both give the
+// Row arithmetic of the attention producer (per-head RMSNorm + partial RoPE)
+// for qkv_append_kernel and the producing decode step, which must give the
 // same bits.  A row is held by a 32-lane half-wave, 8 dims per lane.
 template <bool BF16IN>
 __device__ __forceinline__ void load_row8(const void* base, size_t off, float (&x)[8]) {
@@ -533,7 +532,39 @@ __device__ __forceinline__ float half_wave_sum(float x) {
 
 // RoPE coefficients of the 8 dims d0 .. d0+7 of a lane at position pos:
 // table entries p0 .. p0+7 for rope_dim >= 16, entries 0..3 twice for
-// rope_dim 8; cos 1 / sin 0 outside the rotated dims or with no RoPE.
+// rope_dim 8; cos 1 / sin 0 outside the rotated dims or with no RoPE.  The
+// loads (rope8_load) and the selection (rope8_select) are split so that a
+// caller can issue the loads early and consume them later: every lane of a
+// table loads (lanes outside the rotated dims read valid entries of the same
+// row), so nothing between the two waits on the loads; with no RoPE
+// (half == 0, uniform) nothing is loaded and the selection ignores the
+// registers.
+struct Rope8 {
+    float4 c0, c1, s0, s1;
+};
+__device__ __forceinline__ void rope8_load(const float* rope, int rope_rows, int half, int pos, int d0, Rope8& r) {
+    if (half == 0) return;
+    const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
+    const int o1 = half >= 8 ? 4 : 0;
+    const float* crow = rope + (size_t)pos * half + p0;
+    const float* srow = rope + ((size_t)rope_rows + pos) * half + p0;
+    r.c0 = *reinterpret_cast<const float4*>(crow);
+    r.c1 = *reinterpret_cast<const float4*>(crow + o1);
+    r.s0 = *reinterpret_cast<const float4*>(srow);
+    r.s1 = *reinterpret_cast<const float4*>(srow + o1);
+}
+__device__ __forceinline__ void rope8_select(const Rope8& r, int half, int d0, float (&cs)[8], float (&sn)[8]) {
+    const bool roped = d0 < 2 * half;
+    const float c[8] = {r.c0.x, r.c0.y, r.c0.z, r.c0.w, r.c1.x, r.c1.y, r.c1.z, r.c1.w};
+    const float sv[8] = {r.s0.x, r.s0.y, r.s0.z, r.s0.w, r.s1.x, r.s1.y, r.s1.z, r.s1.w};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        cs[j] = roped ? c[j] : 1.f;
+        sn[j] = roped ? sv[j] : 0.f;
+    }
+}
+// Both in one, for the producer kernel: only the rotated lanes load (its
+// loads are consumed right away).
 __device__ __forceinline__ void load_rope8(const float* rope, int rope_rows, int half, int pos, int d0,
                                            float (&cs)[8], float (&sn)[8]) {
     if (d0 < 2 * half) {
@@ -561,9 +592,7 @@ __device__ __forceinline__ void load_rope8(const float* rope, int rope_rows, int
 // in the half): per-head RMSNorm with weights wn, then partial NeoX RoPE
 // (partner of dim p < half is p + half: lane ^ (half / 8), or inside the
 // lane for rope_dim 8), in the reference's order (src/engine.cpp:3497-3512):
-// (x * r) * w, then x0 c - x1 s and x1 c + x0 s, without contraction.  Both
-// the producer kernel and the fused decode step use it, so they give the same
-// bits.
+// (x * r) * w, then x0 c - x1 s and x1 c + x0 s, without contraction.
 __device__ __forceinline__ void norm_rope_row8(const float (&x)[8], const float (&wn)[8], float eps, int half,
                                                int d0, const float (&cs)[8], const float (&sn)[8], float (&y)[8]) {
 #pragma clang fp contract(off)
@@ -598,6 +627,64 @@ __device__ __forceinline__ void norm_rope_row8(const float (&x)[8], const float 
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) y[j] = z[j];
+    }
+}
+
+// norm_rope_row8 on NR rows at once (row r of each half-wave in x[r]), all
+// with weights wn: the same operations in the same order on each row, so the
+// same bits, but with the rows' dependency chains interleaved and one code
+// path for every RoPE width (the partner lane ^ (half / 8) is fetched with
+// ds_bpermute at a run-time address instead of a ds_swizzle per width).  For
+// code that runs once per launch, where a short instruction stream matters.
+template <int NR>
+__device__ __forceinline__ void norm_rope_rows8(const float (&x)[NR][8], const float (&wn)[8], float eps,
+                                                int half, int d0, const float (&cs)[8], const float (&sn)[8],
+                                                float (&y)[NR][8]) {
+#pragma clang fp contract(off)
+    float ss[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        ss[r] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss[r] += x[r][j] * x[r][j];
+    }
+#pragma unroll
+    for (int r = 0; r < NR; r++) ss[r] = half_wave_sum(ss[r]);
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const float rs = 1.0f / sqrtf(ss[r] / kHeadDim + eps);
+#pragma unroll
+        for (int j = 0; j < 8; j++) y[r][j] = x[r][j] * rs * wn[j];
+    }
+    const bool roped = d0 < 2 * half;
+    if (half >= 8) {  // uniform
+        const int src = (__lane_id() ^ (half >> 3)) << 2;
+        float yp[NR][8];
+#pragma unroll
+        for (int r = 0; r < NR; r++)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                yp[r][j] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(y[r][j])));
+        if (roped) {
+            const bool low = d0 < half;
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    y[r][j] = low ? y[r][j] * cs[j] - yp[r][j] * sn[j] : y[r][j] * cs[j] + yp[r][j] * sn[j];
+        }
+    } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            float z[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                z[j] = y[r][j] * cs[j] - y[r][j + 4] * sn[j];
+                z[j + 4] = y[r][j + 4] * cs[j + 4] + y[r][j] * sn[j + 4];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[r][j] = z[j];
+        }
     }
 }
 
@@ -665,9 +752,11 @@ constexpr int kCombineBatch = 32;
 // 8-B vector store and skips no work.  Points: 0 entry, 1 block walk done,
 // 2 wave merge done, 3 partial stores complete, 4 arrival atomic returned,
 // 5 partials loaded (combiner), 6 folded (combiner), 7 output written (the
-// wave that writes it: the combiner, or every wave of a one-chunk launch).
+// wave that writes it: the combiner, or every wave of a one-chunk launch),
+// 8 q rows built (producing decode step only, after their LDS read-back),
+// 9 q row arithmetic begins (producing decode step only).
 #ifdef KVC_PHASE_STAMPS
-constexpr int kStampWgs = 4096, kStampPoints = 8;
+constexpr int kStampWgs = 4096, kStampPoints = 10;
 __device__ uint64_t phase_stamps[kStampWgs * kWaves * kStampPoints];
 __device__ __forceinline__ void phase_stamp(int point) {
     uint64_t t;
@@ -732,16 +821,17 @@ __device__ __forceinline__ void combine_batch(__amdgpu_buffer_rsrc_t prs, int it
 }
 
 // PRODUCE: the decode step with the attention producer fused in (one query
-// token per sequence, bf16 projection rows a.qkv).  Each wave builds the 4 q
-// rows of its group itself, 2 rows at a time (one per 32-lane half), with the
-// producer's own row arithmetic (norm_rope_row8: per-head RMSNorm + partial
-// RoPE at position L - 1, RNE bf16), stages them in its own slice of sm.acc
-// and reads them back in load_q's layout: no workgroup barrier.  The raw rows,
-// norm weights and RoPE coefficients are requested before the block walk and
-// the arithmetic runs after the walk's first loads are issued (prep).  Wave 0
-// of the workgroup that owns the new position also builds its k row (and
-// stages the raw v row); the fused-append path then folds and appends them
-// from LDS.  The gate is read straight from the projection row.
+// token per sequence, bf16 projection rows a.qkv).  The rows are split over
+// the waves, one row per 32-lane half: waves 0 and 1 build q rows 2w + sub of
+// the group, and wave 2 of the workgroup that owns the new position builds its
+// k row (sub 0) and stages its raw v row (sub 1), all with the producer's row
+// arithmetic (per-head RMSNorm + partial RoPE at position L - 1, RNE bf16;
+// norm_rope_rows8 gives qkv_append_kernel's bits).  The raw rows, weights and
+// RoPE coefficients are requested before the block walk; the arithmetic runs
+// after the walk's first loads are issued (prep), the rows go to LDS
+// (qstage), and after one workgroup barrier every wave reads q in load_q's
+// layout.  The fused-append path then folds and appends k / v from LDS.  The
+// gate is read straight from the projection row.
 template <int NP, bool PRODUCE>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     __shared__ DecodeSmem sm;
@@ -767,14 +857,14 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const bool fused_new = PRODUCE || a.k_new != nullptr;
     const int new_pos = fused_new ? L - 1 : -1;
-    // PRODUCE: wave w's staging rows in LDS (q heads 0..3 of the group, then
-    // k and v of the new token in wave 0); sm.acc is next written by the merge
-    uint16_t* const stage = reinterpret_cast<uint16_t*>(&sm.acc[wave][0][0]);
+    // PRODUCE: the built rows in LDS: q heads 0..3 of the group, then the new
+    // token's k and v
+    __shared__ __align__(16) uint16_t qstage[PRODUCE ? kGroup + 2 : 1][kHeadDim];
     const uint16_t* knew;
     const uint16_t* vnew;
     if constexpr (PRODUCE) {
-        knew = reinterpret_cast<const uint16_t*>(&sm.acc[0][0][0]) + kGroup * kHeadDim;
-        vnew = knew + kHeadDim;
+        knew = qstage[kGroup];
+        vnew = qstage[kGroup + 1];
     } else {
         knew = a.k_new ? a.k_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
         vnew = a.v_new ? a.v_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
@@ -782,59 +872,52 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 
     uint32_t qv[kGroup][2][4];
     // PRODUCE inputs, held from here to prep: lane hl = lane % 32 of half
-    // sub = lane / 32 has dims pd0 .. pd0 + 7 of q rows 2i + sub (raw bf16),
-    // of the k (sub 0) or v (sub 1) row of the new token (owner's wave 0),
-    // their norm weights and the RoPE coefficients of position L - 1
+    // sub = lane / 32 has dims pd0 .. pd0 + 7 of its row (raw bf16), the row's
+    // norm weights and the RoPE coefficients of position L - 1
     const int sub = lane >> 5, pd0 = (lane & 31) * 8;
-    const bool make_new = PRODUCE && wave == 0 && new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
-    u32x4 xq[2], xkv;
-    float wq[8], wk[8], cs[8], sn[8];
+    const bool q_wave = wave < 2;
+    const bool make_new = PRODUCE && wave == 2 && new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
+    u32x4 xr;
+    float wr[8];
+    Rope8 rp;
     if constexpr (PRODUCE) {
-        const uint16_t* prow = a.qkv + (size_t)s * kQkvRow;
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            xq[i] = *reinterpret_cast<const u32x4*>(prow + (size_t)(h * kGroup + 2 * i + sub) * 2 * kHeadDim + pd0);
-        const float4 w0 = *reinterpret_cast<const float4*>(a.q_norm + pd0);
-        const float4 w1 = *reinterpret_cast<const float4*>(a.q_norm + pd0 + 4);
-        wq[0] = w0.x; wq[1] = w0.y; wq[2] = w0.z; wq[3] = w0.w;
-        wq[4] = w1.x; wq[5] = w1.y; wq[6] = w1.z; wq[7] = w1.w;
-        if (make_new) {
+        if (q_wave || make_new) {  // uniform per wave
             constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
-            xkv = *reinterpret_cast<const u32x4*>(prow + kKOff + (size_t)(sub * kKvHeads + h) * kHeadDim + pd0);
-            const float4 k0 = *reinterpret_cast<const float4*>(a.k_norm + pd0);
-            const float4 k1 = *reinterpret_cast<const float4*>(a.k_norm + pd0 + 4);
-            wk[0] = k0.x; wk[1] = k0.y; wk[2] = k0.z; wk[3] = k0.w;
-            wk[4] = k1.x; wk[5] = k1.y; wk[6] = k1.z; wk[7] = k1.w;
+            const size_t ro = q_wave ? (size_t)(h * kGroup + 2 * wave + sub) * 2 * kHeadDim
+                                     : kKOff + (size_t)(sub * kKvHeads + h) * kHeadDim;
+            xr = *reinterpret_cast<const u32x4*>(a.qkv + (size_t)s * kQkvRow + ro + pd0);
+            const float* wrow = (q_wave ? a.q_norm : a.k_norm) + pd0;
+            const float4 w0 = *reinterpret_cast<const float4*>(wrow);
+            const float4 w1 = *reinterpret_cast<const float4*>(wrow + 4);
+            wr[0] = w0.x; wr[1] = w0.y; wr[2] = w0.z; wr[3] = w0.w;
+            wr[4] = w1.x; wr[5] = w1.y; wr[6] = w1.z; wr[7] = w1.w;
+            rope8_load(a.rope, a.rope_rows, a.rope_half, new_pos, pd0, rp);
         }
-        load_rope8(a.rope, a.rope_rows, a.rope_half, new_pos, pd0, cs, sn);
     } else {
         load_q(qv, a.q + ((size_t)s * kQHeads + h * kGroup) * kHeadDim, lane);
     }
     auto prep = [&]() {
         if constexpr (PRODUCE) {
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                float x[8], y[8];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    x[2 * j] = bf16lo(xq[i][j]);
-                    x[2 * j + 1] = bf16hi(xq[i][j]);
-                }
-                norm_rope_row8(x, wq, a.eps, a.rope_half, pd0, cs, sn, y);
-                *reinterpret_cast<u32x4*>(stage + (2 * i + sub) * kHeadDim + pd0) = pack_bf16x8(y);
-            }
-            if (make_new) {  // uniform
-                float x[8], y[8];
+            KVC_STAMP(9);
+            if (q_wave || make_new) {
+                float cs[8], sn[8];
+                rope8_select(rp, a.rope_half, pd0, cs, sn);
+                float x[1][8], y[1][8];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    x[2 * j] = bf16lo(xkv[j]);
-                    x[2 * j + 1] = bf16hi(xkv[j]);
+                    x[0][2 * j] = bf16lo(xr[j]);
+                    x[0][2 * j + 1] = bf16hi(xr[j]);
                 }
-                norm_rope_row8(x, wk, a.eps, a.rope_half, pd0, cs, sn, y);  // half 1 (v): unused
-                *reinterpret_cast<u32x4*>(stage + (kGroup + sub) * kHeadDim + pd0) = sub ? xkv : pack_bf16x8(y);
+                norm_rope_rows8<1>(x, wr, a.eps, a.rope_half, pd0, cs, sn, y);  // v half: unused
+                const int row = q_wave ? 2 * wave + sub : kGroup + sub;
+                *reinterpret_cast<u32x4*>(&qstage[row][pd0]) = make_new && sub ? xr : pack_bf16x8(y[0]);
             }
-            wave_lds_sync();
-            load_q(qv, stage, lane);
+            __syncthreads();
+            load_q(qv, &qstage[0][0], lane);
+#ifdef KVC_PHASE_STAMPS
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+            KVC_STAMP(8);
         }
     };
     WaveState st;
