@@ -479,9 +479,10 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
 }
 
 // ---------------------------------------------------------------------------
-// Row arithmetic of the attention producer (per-head RMSNorm + partial RoPE)
-// for qkv_append_kernel and the producing decode step, which must give the
-// same bits.  A row is held by a 32-lane half-wave, 8 dims per lane.
+// Pieces of the attention producer's row arithmetic (per-head RMSNorm +
+// partial RoPE) used by qkv_append_kernel and by the producing decode step,
+// which must give the same bits.  A row is held by a 32-lane half-wave, 8 dims
+// per lane.
 template <bool BF16IN>
 __device__ __forceinline__ void load_row8(const void* base, size_t off, float (&x)[8]) {
     if constexpr (BF16IN) {
@@ -563,79 +564,17 @@ __device__ __forceinline__ void rope8_select(const Rope8& r, int half, int d0, f
         sn[j] = roped ? sv[j] : 0.f;
     }
 }
-// Both in one, for the producer kernel: only the rotated lanes load (its
-// loads are consumed right away).
-__device__ __forceinline__ void load_rope8(const float* rope, int rope_rows, int half, int pos, int d0,
-                                           float (&cs)[8], float (&sn)[8]) {
-    if (d0 < 2 * half) {
-        const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
-        const float* crow = rope + (size_t)pos * half + p0;
-        const float* srow = rope + ((size_t)rope_rows + pos) * half + p0;
-        const float4 c0 = *reinterpret_cast<const float4*>(crow);
-        const float4 s0 = *reinterpret_cast<const float4*>(srow);
-        const float4 c1 = half >= 8 ? *reinterpret_cast<const float4*>(crow + 4) : c0;
-        const float4 s1 = half >= 8 ? *reinterpret_cast<const float4*>(srow + 4) : s0;
-        cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w;
-        cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
-        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
-        sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            cs[j] = 1.f;
-            sn[j] = 0.f;
-        }
-    }
-}
 
-// One head row held by a 32-lane half-wave, 8 dims per lane (d0 = 8 x lane
-// in the half): per-head RMSNorm with weights wn, then partial NeoX RoPE
-// (partner of dim p < half is p + half: lane ^ (half / 8), or inside the
-// lane for rope_dim 8), in the reference's order (src/engine.cpp:3497-3512):
-// (x * r) * w, then x0 c - x1 s and x1 c + x0 s, without contraction.
-__device__ __forceinline__ void norm_rope_row8(const float (&x)[8], const float (&wn)[8], float eps, int half,
-                                               int d0, const float (&cs)[8], const float (&sn)[8], float (&y)[8]) {
-#pragma clang fp contract(off)
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) ss += x[j] * x[j];
-    ss = half_wave_sum(ss);
-    const float rs = 1.0f / sqrtf(ss / kHeadDim + eps);
-#pragma unroll
-    for (int j = 0; j < 8; j++) y[j] = x[j] * rs * wn[j];
-    const bool roped = d0 < 2 * half;
-    if (half >= 8) {
-        float yp[8];
-        switch (half) {  // partner lane ^ (half / 8), uniform
-            case 8: swap_lanes8<1>(y, yp); break;
-            case 16: swap_lanes8<2>(y, yp); break;
-            case 32: swap_lanes8<4>(y, yp); break;
-            case 64: swap_lanes8<8>(y, yp); break;
-            default: swap_lanes8<16>(y, yp); break;
-        }
-        if (roped) {
-            const bool low = d0 < half;
-#pragma unroll
-            for (int j = 0; j < 8; j++) y[j] = low ? y[j] * cs[j] - yp[j] * sn[j] : y[j] * cs[j] + yp[j] * sn[j];
-        }
-    } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
-        float z[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            z[j] = y[j] * cs[j] - y[j + 4] * sn[j];
-            z[j + 4] = y[j + 4] * cs[j + 4] + y[j] * sn[j + 4];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) y[j] = z[j];
-    }
-}
-
-// norm_rope_row8 on NR rows at once (row r of each half-wave in x[r]), all
-// with weights wn: the same operations in the same order on each row, so the
-// same bits, but with the rows' dependency chains interleaved and one code
-// path for every RoPE width (the partner lane ^ (half / 8) is fetched with
-// ds_bpermute at a run-time address instead of a ds_swizzle per width).  For
-// code that runs once per launch, where a short instruction stream matters.
+// qkv_append_kernel's row arithmetic on NR rows at once (row r of each
+// half-wave in x[r], 8 dims per lane at d0 = 8 x lane in the half), all with
+// weights wn: per-head RMSNorm, then partial NeoX RoPE (partner of dim
+// p < half is p + half: lane ^ (half / 8), or inside the lane for rope_dim
+// 8), in the reference's order (src/engine.cpp:3497-3512): (x * r) * w, then
+// x0 c - x1 s and x1 c + x0 s, without contraction.  The same operations in
+// the same order as the producer kernel, so the same bits; the partner is
+// fetched with ds_bpermute at a run-time address (one code path for every
+// RoPE width, where the producer kernel has a ds_swizzle per width), for code
+// that runs once per launch and should stay short.
 template <int NR>
 __device__ __forceinline__ void norm_rope_rows8(const float (&x)[NR][8], const float (&wn)[8], float eps,
                                                 int half, int d0, const float (&cs)[8], const float (&sn)[8],
@@ -1621,6 +1560,7 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
     const bool kv_wave = wave == kQkvWaves - 1;  // rows 16..19: the kv heads
     constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
     const int half = a.rope_half;
+    const bool roped = d0 < 2 * half;
     const int32_t* trow = a.table + (size_t)a.slot[s] * a.table_stride;
 
     // every input row of this lane, for every token of the workgroup, is
@@ -1649,7 +1589,28 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
                     load_row8<BF16IN>(a.qkv, co + d0, c[tt][i]);
             }
         }
-        load_rope8(a.rope, a.rope_rows, half, a.pos0[s] + tok, d0, cs[tt], sn[tt]);
+        // RoPE coefficients of this lane's 8 dims: table entries p0 .. p0+7
+        // for rope_dim >= 16, entries 0..3 twice for rope_dim 8
+        const int pos = a.pos0[s] + tok;
+        if (roped) {
+            const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
+            const float* crow = a.rope + (size_t)pos * half + p0;
+            const float* srow = a.rope + ((size_t)a.rope_rows + pos) * half + p0;
+            const float4 c0 = *reinterpret_cast<const float4*>(crow);
+            const float4 s0 = *reinterpret_cast<const float4*>(srow);
+            const float4 c1 = half >= 8 ? *reinterpret_cast<const float4*>(crow + 4) : c0;
+            const float4 s1 = half >= 8 ? *reinterpret_cast<const float4*>(srow + 4) : s0;
+            cs[tt][0] = c0.x; cs[tt][1] = c0.y; cs[tt][2] = c0.z; cs[tt][3] = c0.w;
+            cs[tt][4] = c1.x; cs[tt][5] = c1.y; cs[tt][6] = c1.z; cs[tt][7] = c1.w;
+            sn[tt][0] = s0.x; sn[tt][1] = s0.y; sn[tt][2] = s0.z; sn[tt][3] = s0.w;
+            sn[tt][4] = s1.x; sn[tt][5] = s1.y; sn[tt][6] = s1.z; sn[tt][7] = s1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                cs[tt][j] = 1.f;
+                sn[tt][j] = 0.f;
+            }
+        }
     }
     const float* wrow = (kv_wave ? a.k_norm : a.q_norm) + d0;
     const float4 w0 = *reinterpret_cast<const float4*>(wrow);
@@ -1686,8 +1647,39 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int r = wave * 4 + i * 2 + sub;  // 0..15 q heads, 16..19 k heads
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) ss += x[tt][i][j] * x[tt][i][j];
+            ss = half_wave_sum(ss);
+            const float rs = 1.0f / sqrtf(ss / kHeadDim + a.eps);
             float y[8];
-            norm_rope_row8(x[tt][i], wn, a.eps, half, d0, cs[tt], sn[tt], y);
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[j] = x[tt][i][j] * rs * wn[j];
+            if (half >= 8) {
+                float yp[8];
+                switch (half) {  // partner lane ^ (half / 8), uniform
+                    case 8: swap_lanes8<1>(y, yp); break;
+                    case 16: swap_lanes8<2>(y, yp); break;
+                    case 32: swap_lanes8<4>(y, yp); break;
+                    case 64: swap_lanes8<8>(y, yp); break;
+                    default: swap_lanes8<16>(y, yp); break;
+                }
+                if (roped) {
+                    const bool low = d0 < half;
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        y[j] = low ? y[j] * cs[tt][j] - yp[j] * sn[tt][j] : y[j] * cs[tt][j] + yp[j] * sn[tt][j];
+                }
+            } else if (half == 4 && roped) {  // rope_dim 8: pairs inside the lane's dims 0..7
+                float z[8];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    z[j] = y[j] * cs[tt][j] - y[j + 4] * sn[tt][j];
+                    z[j + 4] = y[j + 4] * cs[tt][j + 4] + y[j] * sn[tt][j + 4];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = z[j];
+            }
             if (kv_wave) {
                 const size_t slot =
                     (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;

@@ -127,3 +127,14 @@ def test_phase_stamps_build_runs():
     means = [comb[p]["mean_us"] for p in names]
     assert all(a <= b for a, b in zip(means, means[1:])), means
     assert 0 <= means[0] < means[-1] < 100, means
+    # the one-launch decode step: every wave also stamps the start and the end
+    # of its q row building, between entry and the end of its walk
+    say("bench.py --config b --phases --step-mode fused in a child process")
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--config", "b", "--phases", "--no-cpu",
+                        "--warmup", "8", "--step-mode", "fused"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    d = json.loads(r.stdout.strip().splitlines()[-1])
+    q = d["q_rows"]
+    assert q["arithmetic begins"]["waves"] == 1024 and q["built"]["waves"] == 1024, q
+    assert (d["phases"]["entry"]["mean_us"] <= q["arithmetic begins"]["mean_us"] <= q["built"]["mean_us"]
+            <= d["phases"]["walk done"]["mean_us"]), d

@@ -31,7 +31,7 @@ def _inputs(n, seed):
     return qkv, qn, kn
 
 
-def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0):
+def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0, flags=0):
     """Each prefix length gets two sequences with the same cached K/V; the
     two-launch path runs on the first set, the fused step on the second."""
     h = kvc.hip()
@@ -39,7 +39,7 @@ def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0)
     max_len = 8192
     cfg = kvc.default_config(n_attn_layers=2, n_ssm_layers=0, max_seqs=2 * n, max_seq_len=max_len,
                              pool_blocks=2 * n * (max(prefix) // 32 + 2) + 8, snapshot_slots=0,
-                             alloc_seed=seed, rope_dim=rope_dim, decode_chunk_blocks=chunk_blocks)
+                             alloc_seed=seed, rope_dim=rope_dim, decode_chunk_blocks=chunk_blocks, flags=flags)
     with kvc.Context(cfg) as ctx:
         m = Mirror(2)
         sa = [ctx.seq_create() for _ in prefix]
@@ -117,6 +117,14 @@ def test_decode_step_chunk_sizes():
     for cb in (1, 80):
         say(f"decode step vs two launches, chunk_blocks {cb}")
         run_pair([0, 32, 63, 2600], seed=6400 + cb, chunk_blocks=cb)
+
+
+@pytest.mark.parametrize("flags", [kvc.FLAG_DECODE_SPLIT_D, kvc.FLAG_DECODE_NO_SPLIT_D, kvc.FLAG_EXACT_MATH])
+def test_decode_step_flags(flags):
+    """Both output-dim splits forced on the same lengths, and the exact gate
+    sigmoid instead of the reference's."""
+    say(f"decode step vs two launches, flags {flags:#x}")
+    run_pair([0, 33, 1500], seed=6450 + flags, flags=flags)
 
 
 def test_decode_step_beyond_one_launch():
