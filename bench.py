@@ -587,7 +587,41 @@ def run_d(args):
     ctx.commit(seqs, 1, None, stream)
     L1 = np.array([ctx.seq_len(s) for s in seqs], dtype=np.int64)
     kbytes = bytes_per_layer_d(L1)
-    for b_ in (q, kn, vn, out):
+    # the whole attention step from the projection rows (q/k RMSNorm + RoPE,
+    # k/v append, gated decode): kvc_qkv_append + kvc_decode_attn against
+    # kvc_decode_step
+    qkv = h.malloc(layers * nseq * QKV_ROW * 2)
+    gate = h.malloc(layers * nseq * NQ * D * 2)
+    ctx.fill_normal_bf16(qkv, layers * nseq * QKV_ROW, SEED + 43, 1.0, stream)
+    rng = np.random.default_rng(SEED + 45)
+    q_norm = h.malloc(D * 4).upload(rng.uniform(0.5, 1.5, D).astype(np.float32))
+    k_norm = h.malloc(D * 4).upload(rng.uniform(0.5, 1.5, D).astype(np.float32))
+
+    def attention_step(mode):
+        ctx.reserve(seqs, 1, stream)
+        for layer in range(layers):
+            qkv_l = qkv.ptr + layer * nseq * QKV_ROW * 2
+            q_l, g_l, o_l = (b_.ptr + layer * nseq * NQ * D * 2 for b_ in (q, gate, out))
+            if mode == "two_launch":
+                ctx.qkv_append(layer, seqs, 1, qkv_l, q_norm, k_norm, q_out=q_l, gate_out=g_l,
+                               in_dtype=kvc.DTYPE_BF16, stream=stream)
+                ctx.decode_attn(layer, seqs, q_l, o_l, gate=g_l, out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16,
+                                stream=stream)
+            else:
+                ctx.decode_step(layer, seqs, qkv_l, q_norm, k_norm, o_l, out_dtype=kvc.DTYPE_BF16,
+                                scale=1.0 / 16, stream=stream)
+        ctx.commit(seqs, 1, None, stream)
+
+    step_us = {}
+    for mode in ("two_launch", "fused"):
+        attention_step(mode)
+        h.stream_sync(stream)
+        h.record(e0, stream)
+        for _ in range(steps):
+            attention_step(mode)
+        h.record(e1, stream)
+        step_us[mode] = round(h.elapsed_ms(e0, e1) * 1e3 / (steps * layers), 1)
+    for b_ in (q, kn, vn, out, qkv, gate, q_norm, k_norm):
         b_.free()
     ctx.close()
     res = {"workload": "d: batched paged decode, 64 seqs, ctx U[512,32768] (seeded), block 32, permuted "
@@ -596,7 +630,11 @@ def run_d(args):
            "steps": steps, "mean_ctx": float(L0.mean()),
            "kernel_us": round(kms * 1e3, 1), "kernel_GBps": round(kbytes / (kms * 1e-3) / 1e9, 1),
            "kernel_traffic": profiled_traffic("decode_kernel_d_batched.txt"),
-           "bytes_per_layer": int(bytes_per_layer_d(L0 + 1))}
+           "bytes_per_layer": int(bytes_per_layer_d(L0 + 1)),
+           "attention_step": {"two_launch_us_per_layer": step_us["two_launch"],
+                              "fused_us_per_layer": step_us["fused"],
+                              "note": "the gated attention step of 64 decode tokens from their bf16 projection rows "
+                                      "per layer: kvc_qkv_append + kvc_decode_attn against kvc_decode_step"}}
     if not args.no_cpu:
         rng = np.random.default_rng(SEED + 44)
         sample = rng.choice(Ls, size=min(8, len(Ls)), replace=False)
