@@ -78,6 +78,9 @@ def test_device_ops_fail_loudly_on_host_only_context():
             c.qkv_append(0, [s], 1, 1, 1, 1)
         assert e.value.code == kvc.KVC_ERR_NO_DEVICE
         with pytest.raises(kvc.KvcError) as e:
+            c.decode_step(0, [s], 1, 1, 1, 1)
+        assert e.value.code == kvc.KVC_ERR_NO_DEVICE
+        with pytest.raises(kvc.KvcError) as e:
             c.deltanet_step(0, [s], 1, 1, 1, 1, 1, 1, 1)
         assert e.value.code == kvc.KVC_ERR_NO_DEVICE
         with pytest.raises(kvc.KvcError) as e:
