@@ -231,16 +231,16 @@ int kvc_decode_attn_static(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
  * producer for one token per seq (src/engine.cpp:3485-3525: q/k per-head
  * RMSNorm + partial RoPE at position len + pending - 1, k and v appended
  * there; reserve 1 token) fused into kvc_decode_attn's gated attention
- * (src/engine.cpp:3528-3564, out *= sigmoid(gate)).  qkv: bf16 projection
- * rows [n_seqs][Hq*2*D + 2*Hkv*D] in kvc_qkv_append's layout; q_norm, k_norm:
- * device fp32 [D]; out: [n_seqs][Hq][D] in out_dtype.  Same bits as
- * kvc_qkv_append (bf16 rows, one token) followed by kvc_decode_attn with the
- * produced q and gate and with the appended k / v rows passed as k_new /
- * v_new.  Uses the context's split-K workspace. */
+ * (src/engine.cpp:3528-3564, out *= sigmoid(gate)).  qkv: projection rows
+ * [n_seqs][Hq*2*D + 2*Hkv*D] in kvc_qkv_append's layout, fp32 or bf16 by
+ * in_dtype; q_norm, k_norm: device fp32 [D]; out: [n_seqs][Hq][D] in
+ * out_dtype.  Same bits as kvc_qkv_append (same rows, one token) followed by
+ * kvc_decode_attn with the produced q and gate and with the appended k / v
+ * rows passed as k_new / v_new.  Uses the context's split-K workspace. */
 int kvc_decode_step(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
-                    int32_t n_seqs, const void* qkv, const void* q_norm,
-                    const void* k_norm, void* out, int32_t out_dtype,
-                    float scale, void* stream);
+                    int32_t n_seqs, const void* qkv, int32_t in_dtype,
+                    const void* q_norm, const void* k_norm, void* out,
+                    int32_t out_dtype, float scale, void* stream);
 /* Causal chunked prefill.  The n_q query tokens of seq s sit at positions
  * [len_s + pending_s - n_q, len_s + pending_s) (their K/V appended already);
  * row i attends to keys [0, pos_i].  q/gate: bf16 [n_seqs][n_q][Hq][D];

@@ -1106,6 +1106,7 @@ static int32_t auto_chunk_blocks(kvc_ctx* c, int64_t total_blocks) {
 // The producer inputs of kvc_decode_step (qkv == nullptr: plain decode).
 struct DecodeProducer {
     const void* qkv = nullptr;
+    int32_t in_dtype = KVC_DTYPE_BF16;
     const void* q_norm = nullptr;
     const void* k_norm = nullptr;
 };
@@ -1162,7 +1163,8 @@ static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int
     a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
     a.table = c->d_table;
     if (prod.qkv) {
-        a.qkv = static_cast<const uint16_t*>(prod.qkv) + (size_t)i0 * kQkvRow;
+        a.qkv_f32 = prod.in_dtype == KVC_DTYPE_F32;
+        a.qkv = static_cast<const uint8_t*>(prod.qkv) + (size_t)i0 * kQkvRow * (a.qkv_f32 ? 4 : 2);
         a.q_norm = static_cast<const float*>(prod.q_norm);
         a.k_norm = static_cast<const float*>(prod.k_norm);
         a.rope = c->d_rope;
@@ -1203,6 +1205,8 @@ static int decode_impl(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n
     if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
     if (prod.qkv) {
         if (!prod.q_norm || !prod.k_norm) return set_err(KVC_ERR_INVALID, "decode step needs q_norm and k_norm");
+        if (prod.in_dtype != KVC_DTYPE_F32 && prod.in_dtype != KVC_DTYPE_BF16)
+            return set_err(KVC_ERR_INVALID, "bad in_dtype");
     } else if (!q) {
         return set_err(KVC_ERR_INVALID, "decode needs q and out");
     }
@@ -1235,11 +1239,12 @@ int kvc_decode_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_se
 }
 
 int kvc_decode_step(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, const void* qkv,
-                    const void* q_norm, const void* k_norm, void* out, int32_t out_dtype, float scale,
-                    void* stream) {
+                    int32_t in_dtype, const void* q_norm, const void* k_norm, void* out, int32_t out_dtype,
+                    float scale, void* stream) {
     if (!qkv) return set_err(KVC_ERR_INVALID, "decode step needs qkv");
     DecodeProducer prod;
     prod.qkv = qkv;
+    prod.in_dtype = in_dtype;
     prod.q_norm = q_norm;
     prod.k_norm = k_norm;
     return decode_impl(c, layer, seqs, n_seqs, nullptr, nullptr, nullptr, nullptr, prod, out, out_dtype, scale,

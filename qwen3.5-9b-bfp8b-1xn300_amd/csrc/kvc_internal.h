@@ -91,16 +91,16 @@ struct DecodeArgs {
     int32_t d_parts;        // output-dim parts per (chunk, head): 1 or 2
     int32_t gate_ref;       // 1: the reference's Schraudolph gate sigmoid; 0: exact
     int32_t pad;
-    // decode step with the attention producer fused in (decode_kernel<NP, true>):
+    // decode step with the attention producer fused in (decode_kernel<NP, 1 or 2>):
     // q, gate and the new token's k / v come from the projection rows
-    const uint16_t* qkv;    // bf16 [n_seqs][kQkvRow] (layout of QkvArgs::qkv)
+    const void* qkv;        // [n_seqs][kQkvRow] (layout of QkvArgs::qkv), bf16 or fp32
     const float* q_norm;    // [D]
     const float* k_norm;    // [D]
     const float* rope;      // as QkvArgs::rope
     float eps;
     int32_t rope_half;
     int32_t rope_rows;
-    int32_t pad2;
+    int32_t qkv_f32;        // 1: fp32 rows
     int32_t slot[kMaxBatch];
     int32_t kv_len[kMaxBatch];       // keys attended (new token included)
     int32_t chunk_begin[kMaxBatch + 1];

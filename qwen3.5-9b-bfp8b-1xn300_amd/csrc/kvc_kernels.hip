@@ -759,20 +759,24 @@ __device__ __forceinline__ void combine_batch(__amdgpu_buffer_rsrc_t prs, int it
     }
 }
 
-// PRODUCE: the decode step with the attention producer fused in (one query
-// token per sequence, bf16 projection rows a.qkv).  The rows are split over
+// PROD != 0: the decode step with the attention producer fused in (one query
+// token per sequence, projection rows a.qkv in bf16 (PROD 1) or fp32 (PROD
+// 2), converted as qkv_append_kernel converts them).  The rows are split over
 // the waves, one row per 32-lane half: waves 0 and 1 build q rows 2w + sub of
 // the group, and wave 2 of the workgroup that owns the new position builds its
-// k row (sub 0) and stages its raw v row (sub 1), all with the producer's row
+// k row (sub 0) and stages its v row (sub 1, RNE bf16), all with the producer's row
 // arithmetic (per-head RMSNorm + partial RoPE at position L - 1, RNE bf16;
 // norm_rope_rows8 gives qkv_append_kernel's bits).  The raw rows, weights and
 // RoPE coefficients are requested before the block walk; the arithmetic runs
 // after the walk's first loads are issued (prep), the rows go to LDS
 // (qstage), and after one workgroup barrier every wave reads q in load_q's
 // layout.  The fused-append path then folds and appends k / v from LDS.  The
-// gate is read straight from the projection row.
-template <int NP, bool PRODUCE>
+// gate is read straight from the projection row (fp32 gates rounded to bf16
+// first, as the producer writes them).
+template <int NP, int PROD>
 __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
+    constexpr bool PRODUCE = PROD != 0;
+    constexpr bool F32IN = PROD == 2;
     __shared__ DecodeSmem sm;
     KVC_STAMP(0);
     constexpr int kLanesD = 64 / NP;  // lanes per token subset
@@ -811,20 +815,28 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 
     uint32_t qv[kGroup][2][4];
     // PRODUCE inputs, held from here to prep: lane hl = lane % 32 of half
-    // sub = lane / 32 has dims pd0 .. pd0 + 7 of its row (raw bf16), the row's
-    // norm weights and the RoPE coefficients of position L - 1
+    // sub = lane / 32 has dims pd0 .. pd0 + 7 of its row (raw bf16 in xr[0],
+    // or fp32 in xr[0..1]), the row's norm weights and the RoPE coefficients
+    // of position L - 1
     const int sub = lane >> 5, pd0 = (lane & 31) * 8;
     const bool q_wave = wave < 2;
     const bool make_new = PRODUCE && wave == 2 && new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
-    u32x4 xr;
+    u32x4 xr[F32IN ? 2 : 1];
     float wr[8];
     Rope8 rp;
     if constexpr (PRODUCE) {
         if (q_wave || make_new) {  // uniform per wave
             constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
-            const size_t ro = q_wave ? (size_t)(h * kGroup + 2 * wave + sub) * 2 * kHeadDim
-                                     : kKOff + (size_t)(sub * kKvHeads + h) * kHeadDim;
-            xr = *reinterpret_cast<const u32x4*>(a.qkv + (size_t)s * kQkvRow + ro + pd0);
+            const size_t ro = (size_t)s * kQkvRow + pd0 +
+                              (q_wave ? (size_t)(h * kGroup + 2 * wave + sub) * 2 * kHeadDim
+                                      : kKOff + (size_t)(sub * kKvHeads + h) * kHeadDim);
+            if constexpr (F32IN) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const float*>(a.qkv) + ro);
+                xr[0] = src[0];
+                xr[1] = src[1];
+            } else {
+                xr[0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qkv) + ro);
+            }
             const float* wrow = (q_wave ? a.q_norm : a.k_norm) + pd0;
             const float4 w0 = *reinterpret_cast<const float4*>(wrow);
             const float4 w1 = *reinterpret_cast<const float4*>(wrow + 4);
@@ -844,12 +856,19 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
                 float x[1][8], y[1][8];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    x[0][2 * j] = bf16lo(xr[j]);
-                    x[0][2 * j + 1] = bf16hi(xr[j]);
+                    if constexpr (F32IN) {
+                        x[0][j] = __uint_as_float(xr[0][j]);
+                        x[0][4 + j] = __uint_as_float(xr[1][j]);
+                    } else {
+                        x[0][2 * j] = bf16lo(xr[0][j]);
+                        x[0][2 * j + 1] = bf16hi(xr[0][j]);
+                    }
                 }
                 norm_rope_rows8<1>(x, wr, a.eps, a.rope_half, pd0, cs, sn, y);  // v half: unused
                 const int row = q_wave ? 2 * wave + sub : kGroup + sub;
-                *reinterpret_cast<u32x4*>(&qstage[row][pd0]) = make_new && sub ? xr : pack_bf16x8(y[0]);
+                // the v row: a copy of bf16 input, RNE of fp32 input
+                const u32x4 vrow = F32IN ? pack_bf16x8(x[0]) : xr[0];
+                *reinterpret_cast<u32x4*>(&qstage[row][pd0]) = make_new && sub ? vrow : pack_bf16x8(y[0]);
             }
             __syncthreads();
             load_q(qv, &qstage[0][0], lane);
@@ -929,12 +948,22 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     KVC_STAMP(2);
     const size_t orow = ((size_t)s * kQHeads + h * kGroup + g) * kHeadDim;
     const bool has_gate = PRODUCE || a.gate != nullptr;
-    // gate row of q head h * kGroup + g: its own tensor, or the projection row
-    const uint16_t* grow = PRODUCE ? a.qkv + (size_t)s * kQkvRow + (size_t)(h * kGroup + g) * 2 * kHeadDim + kHeadDim
-                                   : a.gate + orow;
+    // gate of q head h * kGroup + g, dims d0 .. d0 + 3 as packed bf16: from
+    // its own tensor, or from the projection row (fp32 rounded to nearest even)
+    const size_t gro = (size_t)s * kQkvRow + (size_t)(h * kGroup + g) * 2 * kHeadDim + kHeadDim + d0;
+    auto load_gate = [&]() -> uint2 {
+        if constexpr (F32IN) {
+            const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(a.qkv) + gro);
+            return make_uint2(cvt_pk_bf16(f.x, f.y), cvt_pk_bf16(f.z, f.w));
+        } else if constexpr (PRODUCE) {
+            return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.qkv) + gro);
+        } else {
+            return *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+        }
+    };
     uint2 gw = make_uint2(0u, 0u);  // gate words of this thread's dims
     if (n_chunks == 1) {
-        if (has_gate && act) gw = *reinterpret_cast<const uint2*>(grow + d0);
+        if (has_gate && act) gw = load_gate();
         if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lsum, A);
 #ifdef KVC_PHASE_STAMPS
         __builtin_amdgcn_s_waitcnt(0);
@@ -976,7 +1005,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     // arrive while it completes, so a combiner does not wait on them after
     // its fold and no wave waits on them before its arrival
     asm volatile("" ::: "memory");
-    if (has_gate && act) gw = *reinterpret_cast<const uint2*>(grow + d0);
+    if (has_gate && act) gw = load_gate();
     const bool last = __builtin_amdgcn_readfirstlane(prev) == n_chunks - 1;
     KVC_STAMP(4);
     if (!last) return;
@@ -2898,15 +2927,20 @@ int static_scratch(int device, float** part, int32_t** counters) {
 int launch_decode(const DecodeArgs& a, void* stream) {
     const int grid = a.per_xcd * 8;
     const hipStream_t st = (hipStream_t)stream;
-    if (a.qkv) {
+    if (a.qkv && a.qkv_f32) {
         if (a.d_parts == 2)
-            hipLaunchKernelGGL((decode_kernel<2, true>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+            hipLaunchKernelGGL((decode_kernel<2, 2>), dim3(grid), dim3(kWaves * 64), 0, st, a);
         else
-            hipLaunchKernelGGL((decode_kernel<1, true>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+            hipLaunchKernelGGL((decode_kernel<1, 2>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+    } else if (a.qkv) {
+        if (a.d_parts == 2)
+            hipLaunchKernelGGL((decode_kernel<2, 1>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+        else
+            hipLaunchKernelGGL((decode_kernel<1, 1>), dim3(grid), dim3(kWaves * 64), 0, st, a);
     } else if (a.d_parts == 2) {
-        hipLaunchKernelGGL((decode_kernel<2, false>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_kernel<2, 0>), dim3(grid), dim3(kWaves * 64), 0, st, a);
     } else {
-        hipLaunchKernelGGL((decode_kernel<1, false>), dim3(grid), dim3(kWaves * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_kernel<1, 0>), dim3(grid), dim3(kWaves * 64), 0, st, a);
     }
     return (int)hipGetLastError();
 }

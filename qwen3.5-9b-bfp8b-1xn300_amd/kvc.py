@@ -114,7 +114,7 @@ def lib() -> ctypes.CDLL:
             "kvc_qkv_append": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, P, P]),
             "kvc_decode_attn": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
             "kvc_decode_attn_static": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, P, I32, F32, P]),
-            "kvc_decode_step": (ctypes.c_int, [P, I32, pI32, I32, P, P, P, P, I32, F32, P]),
+            "kvc_decode_step": (ctypes.c_int, [P, I32, pI32, I32, P, I32, P, P, P, I32, F32, P]),
             "kvc_kv_checksum": (ctypes.c_int, [P, I32, pI32, I32, P, P]),
             "kvc_prefill_attn": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P, I32, F32, P]),
             "kvc_gather": (ctypes.c_int, [P, I32, pI32, I32, I32, pI32, P, P, P]),
@@ -388,11 +388,12 @@ class Context:
                                              self._p(v_new), self._p(gate), self._p(out), out_dtype,
                                              ctypes.c_float(scale), stream))
 
-    def decode_step(self, layer, seqs, qkv, q_norm, k_norm, out, out_dtype=DTYPE_F32, scale=1.0 / 16,
-                    stream=None):
-        """qkv_append (bf16 rows, one token) + gated decode_attn in one launch"""
-        _check(self.L.kvc_decode_step(self.ptr, layer, _i32(seqs), len(seqs), self._p(qkv), self._p(q_norm),
-                                      self._p(k_norm), self._p(out), out_dtype, ctypes.c_float(scale), stream))
+    def decode_step(self, layer, seqs, qkv, q_norm, k_norm, out, in_dtype=DTYPE_BF16, out_dtype=DTYPE_F32,
+                    scale=1.0 / 16, stream=None):
+        """qkv_append (one token) + gated decode_attn in one launch"""
+        _check(self.L.kvc_decode_step(self.ptr, layer, _i32(seqs), len(seqs), self._p(qkv), in_dtype,
+                                      self._p(q_norm), self._p(k_norm), self._p(out), out_dtype,
+                                      ctypes.c_float(scale), stream))
 
     def prefill_attn(self, layer, seqs, n_q, q, out, gate=None, out_dtype=DTYPE_F32,
                      scale=1.0 / 16, stream=None):

@@ -5,7 +5,7 @@ launch.
 
 Bars:
   - bit-exact against the two-launch path on the same inputs: kvc_qkv_append
-    (bf16 rows, one token) into one copy of each sequence, then
+    (bf16 or fp32 rows, one token) into one copy of each sequence, then
     kvc_decode_attn with the produced q and gate and the appended k / v rows
     as k_new / v_new; the cache after the step (the appended token included)
     is bit-exact too;
@@ -23,15 +23,19 @@ pytestmark = pytest.mark.gpu
 QKV_ROW = NQ * 2 * D + 2 * NKV * D
 
 
-def _inputs(n, seed):
+def _inputs(n, seed, in_dtype=kvc.DTYPE_BF16):
+    """Projection rows in in_dtype (bf16 bit patterns or fp32) and the norm weights."""
     rng = np.random.default_rng(seed)
-    qkv = O.f32_to_bf16(rng.standard_normal((n, QKV_ROW)).astype(np.float32) * 3.0)
+    qkv = rng.standard_normal((n, QKV_ROW)).astype(np.float32) * 3.0
+    if in_dtype == kvc.DTYPE_BF16:
+        qkv = O.f32_to_bf16(qkv)
     qn = rng.uniform(0.5, 1.5, D).astype(np.float32)
     kn = rng.uniform(0.5, 1.5, D).astype(np.float32)
     return qkv, qn, kn
 
 
-def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0, flags=0):
+def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0, flags=0,
+             in_dtype=kvc.DTYPE_BF16):
     """Each prefix length gets two sequences with the same cached K/V; the
     two-launch path runs on the first set, the fused step on the second."""
     h = kvc.hip()
@@ -48,7 +52,7 @@ def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0,
             if p:
                 fill_seq(ctx, m, [a_], p, seed=seed + 3 * p, layers=[1])
                 fill_seq(ctx, m, [b_], p, seed=seed + 3 * p, layers=[1])
-        qkv, qn, kn = _inputs(n, seed + 1)
+        qkv, qn, kn = _inputs(n, seed + 1, in_dtype)
         osz = 2 if out_dtype == kvc.DTYPE_BF16 else 4
         odt = np.uint16 if out_dtype == kvc.DTYPE_BF16 else np.float32
         bq = h.malloc(qkv.nbytes).upload(qkv)
@@ -59,7 +63,7 @@ def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0,
         try:
             # two launches: producer, then decode with the produced rows
             ctx.reserve(sa, 1)
-            ctx.qkv_append(1, sa, 1, bq, bqn, bkn, q_out=qo, gate_out=go, in_dtype=kvc.DTYPE_BF16)
+            ctx.qkv_append(1, sa, 1, bq, bqn, bkn, q_out=qo, gate_out=go, in_dtype=in_dtype)
             ctx.sync()
             lens = [p + 1 for p in prefix]
             kv_a = gather(ctx, 1, sa, lens)
@@ -70,7 +74,7 @@ def run_pair(prefix, seed, rope_dim=64, out_dtype=kvc.DTYPE_F32, chunk_blocks=0,
             ctx.decode_attn(1, sa, qo, o1, k_new=kb, v_new=vb, gate=go, out_dtype=out_dtype)
             # one launch
             ctx.reserve(sb, 1)
-            ctx.decode_step(1, sb, bq, bqn, bkn, o2, out_dtype=out_dtype)
+            ctx.decode_step(1, sb, bq, bqn, bkn, o2, in_dtype=in_dtype, out_dtype=out_dtype)
             ctx.sync()
             out1 = o1.download(odt, (n, NQ, D))
             out2 = o2.download(odt, (n, NQ, D))
@@ -94,6 +98,15 @@ def test_decode_step_bit_exact_single_sequence():
     for p in (0, 1, 31, 32, 33, 64, 1000, 4095):
         say(f"decode step vs two launches, single sequence, prefix {p}")
         run_pair([p], seed=6100 + p)
+
+
+def test_decode_step_fp32_rows():
+    """fp32 projection rows: q / k normalized from fp32, v and gate rounded to
+    bf16 as kvc_qkv_append rounds them; single sequence and a batch."""
+    for prefix in ([0], [31], [4000], [0, 32, 700, 2047, 95]):
+        say(f"decode step vs two launches, fp32 rows, prefix {prefix}")
+        run_pair(prefix, seed=6150 + sum(prefix), in_dtype=kvc.DTYPE_F32)
+    run_pair([5, 1200], seed=6160, in_dtype=kvc.DTYPE_F32, out_dtype=kvc.DTYPE_BF16, rope_dim=8)
 
 
 def test_decode_step_bit_exact_batch():
@@ -134,11 +147,12 @@ def test_decode_step_beyond_one_launch():
     run_pair(prefix, seed=6500)
 
 
-def test_decode_step_matches_oracle():
+@pytest.mark.parametrize("in_dtype", [kvc.DTYPE_BF16, kvc.DTYPE_F32])
+def test_decode_step_matches_oracle(in_dtype):
     prefix = [0, 40, 777]
-    say("decode step vs oracle")
-    m, sb, qkv, qn, kn, q_gpu, out, kv_b = run_pair(prefix, seed=6600)
-    qkv_f = O.bf16_to_f32(qkv)
+    say(f"decode step vs oracle, in_dtype {in_dtype}")
+    m, sb, qkv, qn, kn, q_gpu, out, kv_b = run_pair(prefix, seed=6600 + in_dtype, in_dtype=in_dtype)
+    qkv_f = O.bf16_to_f32(qkv) if in_dtype == kvc.DTYPE_BF16 else qkv
     cos_t, sin_t = O.rope_tables(8192)
     for i, p in enumerate(prefix):
         L = p + 1
@@ -176,6 +190,9 @@ def test_decode_step_errors():
             with pytest.raises(kvc.KvcError) as e:
                 ctx.decode_step(1, [s], bq, bqn, bkn, ob)
             assert e.value.code == kvc.KVC_ERR_RANGE
+            with pytest.raises(kvc.KvcError) as e:
+                ctx.decode_step(0, [s], bq, bqn, bkn, ob, in_dtype=7)
+            assert e.value.code == kvc.KVC_ERR_INVALID
             ctx.decode_step(0, [s], bq, bqn, bkn, ob)
             ctx.sync()
             assert np.all(np.isfinite(ob.download(np.float32, (NQ, D))))
