@@ -328,17 +328,25 @@ __device__ __forceinline__ float gate_sigmoid(float x, int ref) {
     return ref ? sigmoid_ref(x) : sigmoidf_exact(x);
 }
 
-// out row = A / L (* sigmoid(gate)), written as bf16 (RNE) or fp32; gw holds
-// the gate's bf16 values of dims d0 .. d0 + 3 when has_gate.
+// sigmoid(gate) of dims d0 .. d0 + 3 from their bf16 values gw
+__device__ __forceinline__ void gate_factors(uint2 gw, int gate_ref, float (&gs)[4]) {
+    gs[0] = gate_sigmoid(bf16lo(gw.x), gate_ref);
+    gs[1] = gate_sigmoid(bf16hi(gw.x), gate_ref);
+    gs[2] = gate_sigmoid(bf16lo(gw.y), gate_ref);
+    gs[3] = gate_sigmoid(bf16hi(gw.y), gate_ref);
+}
+
+// out row = A / L (* gs, the gate factors of dims d0 .. d0 + 3, when
+// has_gate), written as bf16 (RNE) or fp32.
 __device__ __forceinline__ void write_out(void* out, int out_bf16, size_t row_off, int d0, bool has_gate,
-                                          uint2 gw, int gate_ref, float L, const float (&A)[4]) {
+                                          const float (&gs)[4], float L, const float (&A)[4]) {
     const float inv = __builtin_amdgcn_rcpf(L);
     float o[4] = {A[0] * inv, A[1] * inv, A[2] * inv, A[3] * inv};
     if (has_gate) {
-        o[0] *= gate_sigmoid(bf16lo(gw.x), gate_ref);
-        o[1] *= gate_sigmoid(bf16hi(gw.x), gate_ref);
-        o[2] *= gate_sigmoid(bf16lo(gw.y), gate_ref);
-        o[3] *= gate_sigmoid(bf16hi(gw.y), gate_ref);
+        o[0] *= gs[0];
+        o[1] *= gs[1];
+        o[2] *= gs[2];
+        o[3] *= gs[3];
     }
     if (out_bf16) {
         uint2 w;
@@ -951,20 +959,34 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     // gate of q head h * kGroup + g, dims d0 .. d0 + 3 as packed bf16: from
     // its own tensor, or from the projection row (fp32 rounded to nearest even)
     const size_t gro = (size_t)s * kQkvRow + (size_t)(h * kGroup + g) * 2 * kHeadDim + kHeadDim + d0;
-    auto load_gate = [&]() -> uint2 {
+    // the gate's raw words (fp32 input: 4 floats, rounded when used)
+    u32x4 graw = {0u, 0u, 0u, 0u};
+    auto load_gate = [&]() {
         if constexpr (F32IN) {
-            const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(a.qkv) + gro);
-            return make_uint2(cvt_pk_bf16(f.x, f.y), cvt_pk_bf16(f.z, f.w));
+            graw = *reinterpret_cast<const u32x4*>(static_cast<const float*>(a.qkv) + gro);
         } else if constexpr (PRODUCE) {
-            return *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.qkv) + gro);
+            const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.qkv) + gro);
+            graw[0] = w.x;
+            graw[1] = w.y;
         } else {
-            return *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+            const uint2 w = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+            graw[0] = w.x;
+            graw[1] = w.y;
         }
     };
-    uint2 gw = make_uint2(0u, 0u);  // gate words of this thread's dims
+    // the gate words of this thread's dims as packed bf16
+    auto gate_words = [&](const u32x4& r) -> uint2 {
+        if constexpr (F32IN)
+            return make_uint2(cvt_pk_bf16(__uint_as_float(r[0]), __uint_as_float(r[1])),
+                              cvt_pk_bf16(__uint_as_float(r[2]), __uint_as_float(r[3])));
+        else
+            return make_uint2(r[0], r[1]);
+    };
     if (n_chunks == 1) {
-        if (has_gate && act) gw = load_gate();
-        if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lsum, A);
+        if (has_gate && act) load_gate();
+        float gs[4] = {1.f, 1.f, 1.f, 1.f};
+        if (has_gate) gate_factors(gate_words(graw), a.gate_ref, gs);
+        if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gs, Lsum, A);
 #ifdef KVC_PHASE_STAMPS
         __builtin_amdgcn_s_waitcnt(0);
         KVC_STAMP(7);
@@ -1005,11 +1027,12 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     // arrive while it completes, so a combiner does not wait on them after
     // its fold and no wave waits on them before its arrival
     asm volatile("" ::: "memory");
-    if (has_gate && act) gw = load_gate();
+    if (has_gate && act) load_gate();
     const bool last = __builtin_amdgcn_readfirstlane(prev) == n_chunks - 1;
     KVC_STAMP(4);
     if (!last) return;
     float Mc = kNegBig, Lc = 0.f, Ac[4] = {0.f, 0.f, 0.f, 0.f};
+    float gs[4] = {1.f, 1.f, 1.f, 1.f};  // gate factors (the split-D combine: under its first loads)
     if constexpr (NP == 1) {
         // combine the n_chunks partials of (s, h): wave g takes q head g; every
         // partial of a batch is requested at once (lane k also fetches partial
@@ -1046,6 +1069,15 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
             }
             __builtin_amdgcn_sched_barrier(0);  // keep every load ahead of the first use
             if (k0 == 0) {
+                // the gate words were requested before these loads: their
+                // sigmoids run while the partials are in flight (the empty
+                // asm pins them below the loads)
+                if (has_gate) {
+                    u32x4 g2 = graw;
+                    asm volatile("" : "+v"(g2));
+                    gate_factors(gate_words(g2), a.gate_ref, gs);
+                }
+                __builtin_amdgcn_sched_barrier(0);
                 KVC_STAMP_WAIT_LOADS();
                 KVC_STAMP(5);
             }
@@ -1078,8 +1110,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; j++) Ac[j] = sum_xor32(Ac[j]);
     }
+    if constexpr (NP == 1) {
+        if (has_gate) gate_factors(gate_words(graw), a.gate_ref, gs);
+    }
     KVC_STAMP(6);
-    if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gw, a.gate_ref, Lc, Ac);
+    if (act) write_out(a.out, a.out_bf16, orow, d0, has_gate, gs, Lc, Ac);
     if (lane == 0) *ctr = 0;
 #ifdef KVC_PHASE_STAMPS
     __builtin_amdgcn_s_waitcnt(0);
