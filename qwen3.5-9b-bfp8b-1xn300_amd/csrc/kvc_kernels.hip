@@ -379,7 +379,9 @@ __device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpoo
 // Walk blocks [blk0, blk0 + n_blk) of one (sequence, kv head); keys at
 // positions >= L are masked.  Block ids are fetched once per
 // 64 blocks into a VGPR and read back per block with v_readlane, so no table
-// load sits in the pipeline.  Blocks go in straight-line groups of 4 over 2
+// load sits in the pipeline; the first window's ids (first_ids: lane i holds
+// block blk0 + i, for i < min(64, n_blk)) come from the caller, which
+// requests them before its other loads.  Blocks go in straight-line groups of 4 over 2
 // register buffers (the wait before each compute covers exactly the buffer it
 // reads while the other stays in flight); a window's last 1-3 blocks take a
 // straight-line tail of their own, so no load is ever issued for a block that
@@ -394,7 +396,7 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
                                             const int32_t* __restrict__ trow, int h, int blk0,
                                             int n_blk, int L, const uint32_t (&qv)[kGroup][2][4],
                                             float scale_log2, uint16_t* lds_p, WaveState& st,
-                                            int wave, int lane, int dpart, Prep&& prep) {
+                                            int wave, int lane, int dpart, int first_ids, Prep&& prep) {
     BlockRegs<NP> r0, r1;
     constexpr size_t kUnitElems = (size_t)kBlockTok * kHeadDim;
 #define KVC_LOAD_WIN(R, I)                                                                          \
@@ -435,22 +437,25 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
             KVC_COMPUTE(r0, i + 2);                 \
         }                                           \
     }
-    int wbeg = 0;
+    // the first window is peeled off the loop in both forms, so that its ids
+    // (first_ids) are no loop-carried value: the wait for them then covers
+    // only the loads issued before them
     if constexpr (PREP) {
         // first window: the loads of blocks 0 and 1 (those that exist), prep
         // (inlined once: it runs once per launch, so its code stays small),
         // then the first group or the whole short window
         const int w0 = 0;
         const int wn = min(64, n_blk);
-        const int my_id = lane < wn ? trow[blk0 + lane] : 0;
-        // both block ids are read on every path, so every load issued before
-        // the table's (what prep consumes) is known complete past this point
-        // and prep waits on none of the block loads below
+        const int my_id = first_ids;
+        // blocks 0 and 1 are requested on every path (a short window's
+        // missing ids read 0: block 0 of the pool, loaded and not used), so
+        // the number of loads in flight at prep is fixed and prep waits for
+        // its own inputs without waiting for these
         const int id0 = __builtin_amdgcn_readlane(my_id, 0), id1 = __builtin_amdgcn_readlane(my_id, 1);
-        if (wn >= 1) load_block<NP>(r0, kpool + ((size_t)id0 * kKvHeads + h) * kUnitElems,
-                                    vpool + ((size_t)id0 * kKvHeads + h) * kUnitElems, wave, lane, dpart);
-        if (wn >= 2) load_block<NP>(r1, kpool + ((size_t)id1 * kKvHeads + h) * kUnitElems,
-                                    vpool + ((size_t)id1 * kKvHeads + h) * kUnitElems, wave, lane, dpart);
+        load_block<NP>(r0, kpool + ((size_t)id0 * kKvHeads + h) * kUnitElems,
+                       vpool + ((size_t)id0 * kKvHeads + h) * kUnitElems, wave, lane, dpart);
+        load_block<NP>(r1, kpool + ((size_t)id1 * kKvHeads + h) * kUnitElems,
+                       vpool + ((size_t)id1 * kKvHeads + h) * kUnitElems, wave, lane, dpart);
         prep();
         if (wn >= 4) {
             KVC_COMPUTE(r0, 0);
@@ -472,9 +477,14 @@ __device__ __forceinline__ void walk_blocks(const uint16_t* __restrict__ kpool,
         } else if (wn == 1) {
             KVC_COMPUTE(r0, 0);
         }
-        wbeg = 64;
+    } else if (n_blk > 0) {
+        const int w0 = 0;
+        const int wn = min(64, n_blk);
+        const int my_id = first_ids;
+        int i = 0;
+        KVC_GROUPS
     }
-    for (int w0 = wbeg; w0 < n_blk; w0 += 64) {
+    for (int w0 = 64; w0 < n_blk; w0 += 64) {
         const int wn = min(64, n_blk - w0);
         const int my_id = lane < wn ? trow[blk0 + w0 + lane] : 0;
         int i = 0;
@@ -821,6 +831,17 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
         vnew = a.v_new ? a.v_new + ((size_t)s * kKvHeads + h) * kHeadDim : nullptr;
     }
 
+    // keys [0, Lw) come from the pool; with a fused append the last key
+    // (position L-1) comes from knew/vnew and is folded in by wave 0 of the
+    // chunk that owns it, whose part 0 also writes it into the pool
+    const int Lw = fused_new ? L - 1 : L;
+    const int wblk1 = min(blk1, (Lw + kBlockTok - 1) / kBlockTok);
+    const int n_walk = max(0, wblk1 - blk0);
+    // the first 64 block ids are requested before q: the wait for them (the
+    // load counter completes in order) then does not also wait for q
+    const int first_ids = lane < min(64, n_walk) ? trow[blk0 + lane] : 0;
+    __builtin_amdgcn_sched_barrier(0);
+
     uint32_t qv[kGroup][2][4];
     // PRODUCE inputs, held from here to prep: lane hl = lane % 32 of half
     // sub = lane / 32 has dims pd0 .. pd0 + 7 of its row (raw bf16 in xr[0],
@@ -833,11 +854,15 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     float wr[8];
     Rope8 rp;
     if constexpr (PRODUCE) {
-        if (q_wave || make_new) {  // uniform per wave
+        // every wave loads (the waves that build no row read the group's
+        // first q row), so the loads need no branch and the wait for the
+        // first block ids covers exactly the loads issued before them
+        {
             constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
+            const int qr = q_wave ? 2 * wave + sub : 0;
             const size_t ro = (size_t)s * kQkvRow + pd0 +
-                              (q_wave ? (size_t)(h * kGroup + 2 * wave + sub) * 2 * kHeadDim
-                                      : kKOff + (size_t)(sub * kKvHeads + h) * kHeadDim);
+                              (make_new ? kKOff + (size_t)(sub * kKvHeads + h) * kHeadDim
+                                        : (size_t)(h * kGroup + qr) * 2 * kHeadDim);
             if constexpr (F32IN) {
                 const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const float*>(a.qkv) + ro);
                 xr[0] = src[0];
@@ -845,7 +870,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
             } else {
                 xr[0] = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.qkv) + ro);
             }
-            const float* wrow = (q_wave ? a.q_norm : a.k_norm) + pd0;
+            const float* wrow = (make_new ? a.k_norm : a.q_norm) + pd0;
             const float4 w0 = *reinterpret_cast<const float4*>(wrow);
             const float4 w1 = *reinterpret_cast<const float4*>(wrow + 4);
             wr[0] = w0.x; wr[1] = w0.y; wr[2] = w0.z; wr[3] = w0.w;
@@ -888,13 +913,8 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     };
     WaveState st;
     init_state(st);
-    // keys [0, Lw) come from the pool; with a fused append the last key
-    // (position L-1) comes from knew/vnew and is folded in by wave 0 of the
-    // chunk that owns it, whose part 0 also writes it into the pool
-    const int Lw = fused_new ? L - 1 : L;
-    const int wblk1 = min(blk1, (Lw + kBlockTok - 1) / kBlockTok);
-    walk_blocks<NP, PRODUCE>(a.kpool, a.vpool, trow, h, blk0, max(0, wblk1 - blk0), Lw, qv, a.scale_log2,
-                             sm.p16[wave], st, wave, lane, dpart, prep);
+    walk_blocks<NP, PRODUCE>(a.kpool, a.vpool, trow, h, blk0, n_walk, Lw, qv, a.scale_log2, sm.p16[wave], st,
+                             wave, lane, dpart, first_ids, prep);
     finalize_l(st);
     const bool owns_new = new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
     if (owns_new) {
