@@ -363,16 +363,16 @@ __device__ __forceinline__ void write_out(void* out, int out_bf16, size_t row_of
 // into its pool slot.  Run by the one workgroup whose chunk holds the slot,
 // after its block walk (which never reads that slot), so no store sits inside
 // the load pipeline.
-__device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpool, const int32_t* trow,
-                                                 int h, int pos, const uint16_t* knew,
-                                                 const uint16_t* vnew) {
+// piece = the 16 B of thread t < 64: K piece t (t < 32) or V piece t - 32;
+// blk = the pool block that holds position pos.
+__device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpool, int blk, int h, int pos,
+                                                 const u32x4& piece) {
     const int t = threadIdx.x;
     if (t >= 64) return;
-    const size_t off = (((size_t)trow[pos / kBlockTok] * kKvHeads + h) * kBlockTok + pos % kBlockTok) * kHeadDim;
+    const size_t off = (((size_t)blk * kKvHeads + h) * kBlockTok + pos % kBlockTok) * kHeadDim;
     const int kv = t >> 5, part = t & 31;
-    const uint16_t* src = (kv ? vnew : knew) + part * 8;
     uint16_t* dst = (kv ? vpool : kpool) + off + part * 8;
-    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+    *reinterpret_cast<u32x4*>(dst) = piece;
 }
 
 // ---------------------------------------------------------------------------
@@ -380,8 +380,8 @@ __device__ __forceinline__ void append_new_token(uint16_t* kpool, uint16_t* vpoo
 // positions >= L are masked.  Block ids are fetched once per
 // 64 blocks into a VGPR and read back per block with v_readlane, so no table
 // load sits in the pipeline; the first window's ids (first_ids: lane i holds
-// block blk0 + i, for i < min(64, n_blk)) come from the caller, which
-// requests them before its other loads.  Blocks go in straight-line groups of 4 over 2
+// block blk0 + i, at least for i < min(64, n_blk)) come from the caller,
+// which requests them before its other loads.  Blocks go in straight-line groups of 4 over 2
 // register buffers (the wait before each compute covers exactly the buffer it
 // reads while the other stays in flight); a window's last 1-3 blocks take a
 // straight-line tail of their own, so no load is ever issued for a block that
@@ -645,28 +645,36 @@ __device__ __forceinline__ void norm_rope_rows8(const float (&x)[NR][8], const f
     }
 }
 
-// Fold one extra key (the fused-append token, bf16 rows knew/vnew of this kv
-// head) into a wave's finalized state (uniform m, l).  Each group of 16 lanes
-// holds all 256 dims of q.  Every lane rescales its acc; only the lanes of
-// token subset 0 add p * v (the subsets are summed afterwards).
+// The new key's 8-dim pieces c and c + 16 (c = lane % 16) and this lane's 4
+// dims of the new value (bf16 rows knew / vnew of this kv head), as
+// fold_token_v takes them.
 template <int NP>
-__device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[kGroup][2][4],
-                                           const uint16_t* knew, const uint16_t* vnew,
-                                           float scale_log2, int lane, int dpart) {
+__device__ __forceinline__ void load_new_token(const uint16_t* knew, const uint16_t* vnew, int lane, int dpart,
+                                               u32x4& k0, u32x4& k1, uint2& v) {
     const int c = lane & 15;
-    const uint4 k0 = *reinterpret_cast<const uint4*>(knew + c * 8);
-    const uint4 k1 = *reinterpret_cast<const uint4*>(knew + (c + 16) * 8);
+    k0 = *reinterpret_cast<const u32x4*>(knew + c * 8);
+    k1 = *reinterpret_cast<const u32x4*>(knew + (c + 16) * 8);
+    v = *reinterpret_cast<const uint2*>(vnew + dpart * (kHeadDim / NP) + (lane % (64 / NP)) * 4);
+}
+
+// Fold one extra key (the fused-append token) into a wave's finalized state
+// (uniform m, l).  Each group of 16 lanes holds all 256 dims of q.  Every
+// lane rescales its acc; only the lanes of token subset 0 add p * v (the
+// subsets are summed afterwards).
+template <int NP>
+__device__ __forceinline__ void fold_token_v(WaveState& st, const uint32_t (&qv)[kGroup][2][4], const u32x4& k0,
+                                             const u32x4& k1, uint2 v, float scale_log2, int lane) {
     float sc[kGroup];
 #pragma unroll
     for (int g = 0; g < kGroup; g++) {
-        float x = dot2_bf16(qv[g][0][0], k0.x, 0.f);
-        x = dot2_bf16(qv[g][0][1], k0.y, x);
-        x = dot2_bf16(qv[g][0][2], k0.z, x);
-        x = dot2_bf16(qv[g][0][3], k0.w, x);
-        x = dot2_bf16(qv[g][1][0], k1.x, x);
-        x = dot2_bf16(qv[g][1][1], k1.y, x);
-        x = dot2_bf16(qv[g][1][2], k1.z, x);
-        x = dot2_bf16(qv[g][1][3], k1.w, x);
+        float x = dot2_bf16(qv[g][0][0], k0[0], 0.f);
+        x = dot2_bf16(qv[g][0][1], k0[1], x);
+        x = dot2_bf16(qv[g][0][2], k0[2], x);
+        x = dot2_bf16(qv[g][0][3], k0[3], x);
+        x = dot2_bf16(qv[g][1][0], k1[0], x);
+        x = dot2_bf16(qv[g][1][1], k1[1], x);
+        x = dot2_bf16(qv[g][1][2], k1[2], x);
+        x = dot2_bf16(qv[g][1][3], k1[3], x);
         x += dpp<kDppXor1>(x);
         x += dpp<kDppXor2>(x);
         x += dpp<kDppHalfMirror>(x);  // after xor 1, 2 every lane of a quad agrees
@@ -674,9 +682,7 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
         sc[g] = readlane(x, 0) * scale_log2;
     }
     constexpr int kLanesD = 64 / NP;
-    const int dl = lane % kLanesD;
     const float vs = lane < kLanesD ? 1.f : 0.f;
-    const uint2 v = *reinterpret_cast<const uint2*>(vnew + dpart * (kHeadDim / NP) + dl * 4);
     const float vf[4] = {bf16lo(v.x) * vs, bf16hi(v.x) * vs, bf16lo(v.y) * vs, bf16hi(v.y) * vs};
 #pragma unroll
     for (int g = 0; g < kGroup; g++) {
@@ -688,6 +694,16 @@ __device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[k
         for (int j = 0; j < 4; j++) st.acc[g][j] = fmaf(st.acc[g][j], cg, p * vf[j]);
         st.m[g] = mn;
     }
+}
+
+template <int NP>
+__device__ __forceinline__ void fold_token(WaveState& st, const uint32_t (&qv)[kGroup][2][4],
+                                           const uint16_t* knew, const uint16_t* vnew,
+                                           float scale_log2, int lane, int dpart) {
+    u32x4 k0, k1;
+    uint2 v;
+    load_new_token<NP>(knew, vnew, lane, dpart, k0, k1, v);
+    fold_token_v<NP>(st, qv, k0, k1, v, scale_log2, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -837,9 +853,10 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     const int Lw = fused_new ? L - 1 : L;
     const int wblk1 = min(blk1, (Lw + kBlockTok - 1) / kBlockTok);
     const int n_walk = max(0, wblk1 - blk0);
-    // the first 64 block ids are requested before q: the wait for them (the
-    // load counter completes in order) then does not also wait for q
-    const int first_ids = lane < min(64, n_walk) ? trow[blk0 + lane] : 0;
+    // the ids of the chunk's first 64 blocks (the walk's and the new token's)
+    // are requested before q: the wait for them (the load counter completes
+    // in order) then does not also wait for q
+    const int first_ids = lane < min(64, blk1 - blk0) ? trow[blk0 + lane] : 0;
     __builtin_amdgcn_sched_barrier(0);
 
     uint32_t qv[kGroup][2][4];
@@ -918,10 +935,16 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
     finalize_l(st);
     const bool owns_new = new_pos >= blk0 * kBlockTok && new_pos < blk1 * kBlockTok;
     if (owns_new) {
-        if (wave == 0) fold_token<NP>(st, qv, knew, vnew, a.scale_log2, lane, dpart);
-        if (dpart == 0)
-            append_new_token(const_cast<uint16_t*>(a.kpool), const_cast<uint16_t*>(a.vpool), trow, h, new_pos,
-                             knew, vnew);
+        // the new token's block id: from the chunk's ids (read before q) when
+        // it is among the first 64
+        const int nb = new_pos / kBlockTok - blk0;
+        const int blk = nb < 64 ? __builtin_amdgcn_readlane(first_ids, nb) : trow[new_pos / kBlockTok];
+        if (wave == 0) {
+            fold_token<NP>(st, qv, knew, vnew, a.scale_log2, lane, dpart);
+            if (dpart == 0)
+                append_new_token(const_cast<uint16_t*>(a.kpool), const_cast<uint16_t*>(a.vpool), blk, h, new_pos,
+                                 *reinterpret_cast<const u32x4*>(((lane >> 5) ? vnew : knew) + (lane & 31) * 8));
+        }
     }
     KVC_STAMP(1);
 
