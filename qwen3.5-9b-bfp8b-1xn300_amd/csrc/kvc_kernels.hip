@@ -1306,6 +1306,14 @@ void prefill_mfma_kernel(PrefillArgs a) {
     const float c = fabsf(a.scale_log2);
     const uint32_t qflip = a.scale_log2 < 0.f ? 0x80008000u : 0u;
 
+    // block ids of a 64-block window sit in one VGPR (lane i = block w0 + i)
+    // and are read with v_readlane: no dependent table load on the fetch
+    // path.  The first window's are requested before Q, so the wait for them
+    // (the load counter completes in order) does not also wait for Q.
+    int idw0 = 0;
+    int idv = lane < n_blocks ? trow[lane] : 0;
+    __builtin_amdgcn_sched_barrier(0);
+
     // Q^T as the B operand: qb[nt][ks] = q[row rw0 + 16nt + r16][d 32ks + 8q4 .. +7]
     bf16x8_t qb[NT][8];
 #pragma unroll
@@ -1323,10 +1331,6 @@ void prefill_mfma_kernel(PrefillArgs a) {
         }
     }
 
-    // block ids of a 64-block window sit in one VGPR (lane i = block w0 + i)
-    // and are read with v_readlane: no dependent table load on the fetch path
-    int idw0 = 0;
-    int idv = lane < n_blocks ? trow[lane] : 0;
     // wave w loads tile rows kLoadRows*w .., two per instruction (lanes 0-31:
     // row r0, lanes 32-63: the next row); lane l fills chunk position l % 32
     // of its row, i.e. global chunk (l % 32) ^ swz(row).  A wave's rows lie in
