@@ -986,6 +986,7 @@ def run_phases(args, launches=40):
         crows = {p: [] for p in PHASE_POINTS}
         prep_rows = []  # point 8: q rows built (producing decode step)
         prep0_rows = []  # point 9: their arithmetic begins
+        barrier_rows = []  # point 10: the wave merge's barrier passed
         for it in range(launches):
             r = it % B.reps
             stamps.zero()
@@ -1007,6 +1008,10 @@ def run_phases(args, launches=40):
                     rows[p].append((us[:, :, i][sel].mean(), us[:, :, i][sel].max(), int(sel.sum())))
                 if comb.any():
                     crows[p].append((us[:, :, i][comb].mean(), us[:, :, i][comb].max(), int(comb.sum())))
+            if npt > 10:
+                sel = live & (t[:, :, 10] >= t[:, :, 0])
+                if sel.any():
+                    barrier_rows.append((us[:, :, 10][sel].mean(), us[:, :, 10][sel].max(), int(sel.sum())))
             if npt > len(PHASE_POINTS):
                 sel = live & (t[:, :, 8] >= t[:, :, 0])
                 if sel.any():
@@ -1027,6 +1032,8 @@ def run_phases(args, launches=40):
            "combining_waves": summary(crows)}
     if prep_rows:
         res["q_rows"] = summary({"arithmetic begins": prep0_rows, "built": prep_rows})
+    if barrier_rows:
+        res["merge_barrier_passed"] = summary({"all waves": barrier_rows})["all waves"]
     return res
 
 

@@ -727,9 +727,10 @@ constexpr int kCombineBatch = 32;
 // 5 partials loaded (combiner), 6 folded (combiner), 7 output written (the
 // wave that writes it: the combiner, or every wave of a one-chunk launch),
 // 8 q rows built (producing decode step only, after their LDS read-back),
-// 9 q row arithmetic begins (producing decode step only).
+// 9 q row arithmetic begins (producing decode step only), 10 the wave merge's
+// barrier passed (two-part launches).
 #ifdef KVC_PHASE_STAMPS
-constexpr int kStampWgs = 4096, kStampPoints = 10;
+constexpr int kStampWgs = 4096, kStampPoints = 11;
 __device__ uint64_t phase_stamps[kStampWgs * kWaves * kStampPoints];
 __device__ __forceinline__ void phase_stamp(int point) {
     uint64_t t;
@@ -979,6 +980,7 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
             }
         }
         __syncthreads();
+        KVC_STAMP(10);
         M = kNegBig;
 #pragma unroll
         for (int w = 0; w < kWaves; w++) M = fmaxf(M, sm.ml[w][g][0]);

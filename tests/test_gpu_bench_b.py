@@ -127,6 +127,10 @@ def test_phase_stamps_build_runs():
     means = [comb[p]["mean_us"] for p in names]
     assert all(a <= b for a, b in zip(means, means[1:])), means
     assert 0 <= means[0] < means[-1] < 100, means
+    # every wave of the two-part launch stamps its pass of the merge barrier
+    mb = d["merge_barrier_passed"]
+    assert mb["waves"] == 1024, mb
+    assert allw["walk done"]["mean_us"] <= mb["mean_us"] <= allw["merge done"]["mean_us"], (mb, allw)
     # the one-launch decode step: every wave also stamps the start and the end
     # of its q row building, between entry and the end of its walk
     say("bench.py --config b --phases --step-mode fused in a child process")
