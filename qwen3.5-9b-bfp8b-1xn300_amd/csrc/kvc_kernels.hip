@@ -553,16 +553,16 @@ __device__ __forceinline__ float half_wave_sum(float x) {
 // table entries p0 .. p0+7 for rope_dim >= 16, entries 0..3 twice for
 // rope_dim 8; cos 1 / sin 0 outside the rotated dims or with no RoPE.  The
 // loads (rope8_load) and the selection (rope8_select) are split so that a
-// caller can issue the loads early and consume them later: every lane of a
-// table loads (lanes outside the rotated dims read valid entries of the same
-// row), so nothing between the two waits on the loads; with no RoPE
-// (half == 0, uniform) nothing is loaded and the selection ignores the
-// registers.
+// caller can issue the loads early and consume them later: every lane loads,
+// on every path (lanes outside the rotated dims read valid entries of the same
+// row; with no RoPE, half == 0, the loads read the first 16 B of `rope`, which
+// must then still point at valid memory, and the selection ignores them), so
+// nothing between the two waits on the loads and the number of loads in
+// flight does not depend on the RoPE width.
 struct Rope8 {
     float4 c0, c1, s0, s1;
 };
 __device__ __forceinline__ void rope8_load(const float* rope, int rope_rows, int half, int pos, int d0, Rope8& r) {
-    if (half == 0) return;
     const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
     const int o1 = half >= 8 ? 4 : 0;
     const float* crow = rope + (size_t)pos * half + p0;
@@ -893,8 +893,11 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
             const float4 w1 = *reinterpret_cast<const float4*>(wrow + 4);
             wr[0] = w0.x; wr[1] = w0.y; wr[2] = w0.z; wr[3] = w0.w;
             wr[4] = w1.x; wr[5] = w1.y; wr[6] = w1.z; wr[7] = w1.w;
-            rope8_load(a.rope, a.rope_rows, a.rope_half, new_pos, pd0, rp);
+            rope8_load(a.rope_half ? a.rope : a.q_norm, a.rope_rows, a.rope_half, new_pos, pd0, rp);
         }
+        // keep these loads here, ahead of the walk's (the compiler would
+        // otherwise move them to their first use, behind the block loads)
+        asm volatile("" ::: "memory");
     } else {
         load_q(qv, a.q + ((size_t)s * kQHeads + h * kGroup) * kHeadDim, lane);
     }
