@@ -22,6 +22,9 @@
  *                               src/engine.cpp:3485-3564
  *   kvc_prefill_attn            per-token causal attention of a prefill batch,
  *                               src/engine.cpp:2892-2924
+ *   kvc_prefill_step            the producer and the prefill attention of a
+ *                               chunk, q and gate built inside the attention,
+ *                               src/engine.cpp:2846-2924
  *   kvc_gather                  reads the cache in the reference layout
  *                               [pos][kv_head][d], src/engine.cpp:3539
  *   kvc_state_ptrs              g_ssm_state / g_conv_state, src/engine.cpp:86-94
@@ -249,6 +252,19 @@ int kvc_prefill_attn(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
                      int32_t n_seqs, int32_t n_q, const void* q,
                      const void* gate, void* out, int32_t out_dtype,
                      float scale, void* stream);
+/* A prefill chunk's attention step from its projection rows: kvc_qkv_append's
+ * producer (src/engine.cpp:2846-2889: k and v normalized / rotated and
+ * appended at the chunk's pending positions) and kvc_prefill_attn's gated
+ * causal attention (src/engine.cpp:2892-2924), with q and the gate built from
+ * the rows inside the attention launch instead of going through memory.
+ * qkv: [n_seqs][n_q][Hq*2*D + 2*Hkv*D] in kvc_qkv_append's layout, fp32 or
+ * bf16 by in_dtype; q_norm, k_norm: device fp32 [D]; out: [n_seqs][n_q][Hq][D]
+ * in out_dtype.  Same bits (output and cache) as kvc_qkv_append with q_out and
+ * gate_out followed by kvc_prefill_attn on them.  Two launches. */
+int kvc_prefill_step(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
+                     int32_t n_seqs, int32_t n_q, const void* qkv,
+                     int32_t in_dtype, const void* q_norm, const void* k_norm,
+                     void* out, int32_t out_dtype, float scale, void* stream);
 /* Copy positions [tok0, tok0 + n_tok[s]) of each seq into contiguous bf16
  * [n_tok][Hkv][D] (the reference cache layout); outputs are packed back to
  * back in seq order.  Bit-exact. */

@@ -1260,20 +1260,15 @@ int kvc_decode_attn_static(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32
                        kStaticItems, "static decode workspace");
 }
 
-int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t n_q, const void* q,
-                     const void* gate, void* out, int32_t out_dtype, float scale, void* stream) {
-    if (!c) return set_err(KVC_ERR_INVALID, "null context");
-    int rc;
-    if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
-    if (!q || !out || n_q <= 0) return set_err(KVC_ERR_INVALID, "prefill needs q, out and n_q > 0");
-    if (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16) return set_err(KVC_ERR_INVALID, "bad out_dtype");
-    if (!std::isfinite(scale)) return set_err(KVC_ERR_INVALID, "scale must be finite");
-    for (int32_t i = 0; i < n_seqs; i++)
-        if (c->seqs[seqs[i]].pending < n_q)
-            return set_err(KVC_ERR_STATE, "sequence %d: prefill of %d rows but %d reserved", seqs[i], n_q,
-                           c->seqs[seqs[i]].pending);
+// Prefill launches over all seqs, 64 per launch (arguments checked by the
+// caller).  With qkv (the prefill step), q and gate come from the projection
+// rows instead of q / gate.
+static int prefill_launches(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t n_q,
+                            const void* q, const void* gate, const void* qkv, int32_t in_dtype, const void* q_norm,
+                            void* out, int32_t out_dtype, float scale, void* stream) {
     const size_t qrow = (size_t)n_q * kQHeads * kHeadDim;
     const size_t osz = out_dtype == KVC_DTYPE_BF16 ? 2 : 4;
+    const size_t isz = in_dtype == KVC_DTYPE_F32 ? 4 : 2;
     for (int32_t i0 = 0; i0 < n_seqs; i0 += kMaxBatch) {
         const int32_t n = std::min(kMaxBatch, n_seqs - i0);
         PrefillArgs a{};
@@ -1285,8 +1280,18 @@ int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_s
         a.kpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2) * c->layer_kv_bytes);
         a.vpool = reinterpret_cast<const uint16_t*>(c->d_pool + (int64_t)(layer * 2 + 1) * c->layer_kv_bytes);
         a.table = c->d_table;
-        a.q = static_cast<const uint16_t*>(q) + (size_t)i0 * qrow;
-        a.gate = gate ? static_cast<const uint16_t*>(gate) + (size_t)i0 * qrow : nullptr;
+        if (qkv) {
+            a.qkv = static_cast<const uint8_t*>(qkv) + (size_t)i0 * n_q * kQkvRow * isz;
+            a.qkv_f32 = in_dtype == KVC_DTYPE_F32;
+            a.q_norm = static_cast<const float*>(q_norm);
+            a.rope = c->d_rope;
+            a.eps = c->cfg.rms_norm_eps;
+            a.rope_half = c->cfg.rope_dim / 2;
+            a.rope_rows = c->cfg.max_seq_len;
+        } else {
+            a.q = static_cast<const uint16_t*>(q) + (size_t)i0 * qrow;
+            a.gate = gate ? static_cast<const uint16_t*>(gate) + (size_t)i0 * qrow : nullptr;
+        }
         a.out = static_cast<uint8_t*>(out) + (size_t)i0 * qrow * osz;
         a.scale_log2 = scale * 1.4426950408889634f;
         a.out_bf16 = out_dtype == KVC_DTYPE_BF16;
@@ -1302,6 +1307,46 @@ int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_s
         if (e) return hip_err((hipError_t)e, "prefill launch");
     }
     return KVC_OK;
+}
+
+static int check_prefill(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t n_q, void* out,
+                         int32_t out_dtype, float scale) {
+    int rc;
+    if ((rc = check_device(c)) || (rc = check_layer(c, layer)) || (rc = check_seqs(c, seqs, n_seqs))) return rc;
+    if (!out || n_q <= 0) return set_err(KVC_ERR_INVALID, "prefill needs q, out and n_q > 0");
+    if (out_dtype != KVC_DTYPE_F32 && out_dtype != KVC_DTYPE_BF16) return set_err(KVC_ERR_INVALID, "bad out_dtype");
+    if (!std::isfinite(scale)) return set_err(KVC_ERR_INVALID, "scale must be finite");
+    for (int32_t i = 0; i < n_seqs; i++)
+        if (c->seqs[seqs[i]].pending < n_q)
+            return set_err(KVC_ERR_STATE, "sequence %d: prefill of %d rows but %d reserved", seqs[i], n_q,
+                           c->seqs[seqs[i]].pending);
+    return KVC_OK;
+}
+
+int kvc_prefill_attn(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t n_q, const void* q,
+                     const void* gate, void* out, int32_t out_dtype, float scale, void* stream) {
+    if (!c) return set_err(KVC_ERR_INVALID, "null context");
+    if (!q) return set_err(KVC_ERR_INVALID, "prefill needs q, out and n_q > 0");
+    int rc;
+    if ((rc = check_prefill(c, layer, seqs, n_seqs, n_q, out, out_dtype, scale))) return rc;
+    return prefill_launches(c, layer, seqs, n_seqs, n_q, q, gate, nullptr, KVC_DTYPE_BF16, nullptr, out, out_dtype,
+                            scale, stream);
+}
+
+int kvc_prefill_step(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t n_q, const void* qkv,
+                     int32_t in_dtype, const void* q_norm, const void* k_norm, void* out, int32_t out_dtype,
+                     float scale, void* stream) {
+    if (!c) return set_err(KVC_ERR_INVALID, "null context");
+    if (!qkv || !q_norm || !k_norm) return set_err(KVC_ERR_INVALID, "prefill step needs qkv, q_norm and k_norm");
+    if (in_dtype != KVC_DTYPE_F32 && in_dtype != KVC_DTYPE_BF16) return set_err(KVC_ERR_INVALID, "bad in_dtype");
+    int rc;
+    if ((rc = check_prefill(c, layer, seqs, n_seqs, n_q, out, out_dtype, scale))) return rc;
+    // the K/V side of the producer (kvc_qkv_append with no q / gate output),
+    // then the attention with q and gate built from the rows
+    if ((rc = kvc_qkv_append(c, layer, seqs, n_seqs, n_q, qkv, in_dtype, q_norm, k_norm, nullptr, nullptr, stream)))
+        return rc;
+    return prefill_launches(c, layer, seqs, n_seqs, n_q, nullptr, nullptr, qkv, in_dtype, q_norm, out, out_dtype,
+                            scale, stream);
 }
 
 int kvc_gather(kvc_ctx* c, int32_t layer, const int32_t* seqs, int32_t n_seqs, int32_t tok0, const int32_t* n_tok,

@@ -231,6 +231,15 @@ struct PrefillArgs {
     int32_t gate_ref;           // 1: the reference's Schraudolph gate sigmoid; 0: exact
     int32_t n_groups;           // n_seqs * Hkv (sequence, kv head) groups
     int32_t pad2;
+    // prefill with the producer's q side fused in (prefill_mfma_kernel<NT, 1 or 2>):
+    // q and gate come from the projection rows
+    const void* qkv;            // [n_seqs][n_q][kQkvRow] (layout of QkvArgs::qkv), bf16 or fp32
+    const float* q_norm;        // [D]
+    const float* rope;          // as QkvArgs::rope
+    float eps;
+    int32_t rope_half;
+    int32_t rope_rows;
+    int32_t qkv_f32;            // 1: fp32 rows
     int32_t slot[kMaxBatch];
     int32_t q_pos0[kMaxBatch];  // position of query row 0
     int32_t seq_order[kMaxBatch];  // batch indices, most keys first

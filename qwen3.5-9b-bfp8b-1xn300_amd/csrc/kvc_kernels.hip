@@ -1254,6 +1254,142 @@ __device__ __forceinline__ u32x2 lds_load_tr16(uint32_t base, uint32_t off) {
 }
 
 
+// a compile-time integer as a value (tile buffer index, register distance)
+template <int B>
+struct PfBuf {
+    static constexpr int value = B;
+};
+
+// One q row of the prefill step in the prefill's B-operand layout: lane (q4,
+// r16) holds dims 32 ks + 8 q4 .. +7 (ks = 0..7) of its row, so a row's 256
+// dims sit on lanes r16, r16 + 16, r16 + 32, r16 + 48.  The arithmetic is
+// qkv_append_kernel's (per-head RMSNorm, partial NeoX RoPE at position pos,
+// RNE bf16; src/engine.cpp:2861-2883), with its bits: the sum of squares
+// takes the producer's tree (each 8-dim group g = d / 8 summed in order, then
+// the groups paired by bit 0 of g, bit 1, ..., bit 4, as its half-wave sum
+// pairs lanes ^ 1, ^ 2, the half-row mirror, the row rotate by 8 and ^ 16);
+// here bits 0 and 1 of g are lane bits 4 and 5 and bits 2..4 are ks.  The
+// RoPE partner of dim d < half is d + half: register ks ^ (half / 32) for
+// half >= 32, lane ^ 16 / ^ 32 for half 8 / 16, the lane's own dims for half
+// 4.  qb receives the bf16 words XOR qflip (the sign of a negative scale).
+template <bool F32IN>
+__device__ __forceinline__ void prefill_q_row(const void* qkv, size_t row, const float* q_norm,
+                                              const float* rope, int rope_rows, int half, int pos, float eps,
+                                              int q4, uint32_t qflip, bf16x8_t (&qb)[8]) {
+#pragma clang fp contract(off)
+    float x[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        const size_t e = row + 32 * ks + 8 * q4;
+        if constexpr (F32IN) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const float*>(qkv) + e);
+            const u32x4 f0 = src[0], f1 = src[1];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                x[ks][j] = __uint_as_float(f0[j]);
+                x[ks][4 + j] = __uint_as_float(f1[j]);
+            }
+        } else {
+            const u32x4 u = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(qkv) + e);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                x[ks][2 * j] = bf16lo(u[j]);
+                x[ks][2 * j + 1] = bf16hi(u[j]);
+            }
+        }
+    }
+    float gs[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        gs[ks] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) gs[ks] += x[ks][j] * x[ks][j];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) gs[ks] += shfl_xor<16>(gs[ks]);
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) gs[ks] += shfl_xor<32>(gs[ks]);
+    const float ss = ((gs[0] + gs[1]) + (gs[2] + gs[3])) + ((gs[4] + gs[5]) + (gs[6] + gs[7]));
+    const float rs = 1.0f / sqrtf(ss / kHeadDim + eps);
+    float y[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        const float4 w0 = *reinterpret_cast<const float4*>(q_norm + 32 * ks + 8 * q4);
+        const float4 w1 = *reinterpret_cast<const float4*>(q_norm + 32 * ks + 8 * q4 + 4);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int j = 0; j < 8; j++) y[ks][j] = x[ks][j] * rs * w[j];
+    }
+    // RoPE coefficients of dims d0 .. d0 + 7 (d0 = 32 ks + 8 q4 < 2 half):
+    // entries p0 .. p0 + 7 of the position's row (entries 0..3 twice for half 4)
+    auto coef = [&](int d0, float (&c)[8], float (&sn)[8]) {
+        const int p0 = half >= 8 ? (d0 & (half - 1)) : 0;
+        const int o1 = half >= 8 ? 4 : 0;
+        const float* crow = rope + (size_t)pos * half + p0;
+        const float* srow = rope + ((size_t)rope_rows + pos) * half + p0;
+        const float4 c0 = *reinterpret_cast<const float4*>(crow);
+        const float4 c1 = *reinterpret_cast<const float4*>(crow + o1);
+        const float4 s0 = *reinterpret_cast<const float4*>(srow);
+        const float4 s1 = *reinterpret_cast<const float4*>(srow + o1);
+        c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+    };
+    // half >= 32: registers ks < 2 PM rotate, partner register ks ^ PM
+    auto rotate_regs = [&](auto pmc) {
+        constexpr int PM = decltype(pmc)::value;
+        float z[2 * PM][8];
+#pragma unroll
+        for (int ks = 0; ks < 2 * PM; ks++) {
+            float c[8], sn[8];
+            coef(32 * ks + 8 * q4, c, sn);
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                z[ks][j] = ks < PM ? y[ks][j] * c[j] - y[ks ^ PM][j] * sn[j] : y[ks][j] * c[j] + y[ks ^ PM][j] * sn[j];
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2 * PM; ks++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[ks][j] = z[ks][j];
+    };
+    if (half == 32) {  // uniform
+        rotate_regs(PfBuf<1>{});
+    } else if (half == 64) {
+        rotate_regs(PfBuf<2>{});
+    } else if (half == 128) {
+        rotate_regs(PfBuf<4>{});
+    } else if (half >= 8) {  // 8 or 16: register 0 only, partner lane ^ 16 (half 8) or ^ 32 (half 16)
+        float yp[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) yp[j] = half == 8 ? shfl_xor<16>(y[0][j]) : shfl_xor<32>(y[0][j]);
+        const int d0 = 8 * q4;
+        if (d0 < 2 * half) {
+            float c[8], sn[8];
+            coef(d0, c, sn);
+            const bool low = d0 < half;
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[0][j] = low ? y[0][j] * c[j] - yp[j] * sn[j] : y[0][j] * c[j] + yp[j] * sn[j];
+        }
+    } else if (half == 4 && q4 == 0) {  // rope_dim 8: pairs (j, j + 4) inside the lane's dims 0..7
+        float c[8], sn[8];
+        coef(0, c, sn);
+        float z[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            z[j] = y[0][j] * c[j] - y[0][j + 4] * sn[j];
+            z[j + 4] = y[0][j + 4] * c[j + 4] + y[0][j] * sn[j + 4];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) y[0][j] = z[j];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = cvt_pk_bf16(y[ks][2 * i], y[ks][2 * i + 1]) ^ qflip;
+        qb[ks] = as_bf16x8(w);
+    }
+}
+
 // NT = 16-row query tiles per wave: NT = 2 runs 4 waves (one per q head of
 // the group, 32 rows each); NT = 1 runs 8 waves (q head, row half), two per
 // SIMD, so one wave's MFMAs overlap the other's LDS reads and softmax.
@@ -1271,14 +1407,18 @@ __device__ __forceinline__ u32x2 lds_load_tr16(uint32_t base, uint32_t off) {
 //  - the softmax denominator comes from two more MFMAs per tile, with an
 //    all-ones A operand against the same bf16 P^T (so it sums exactly the
 //    weights that P.V uses).
-template <int B>
-struct PfBuf {
-    static constexpr int value = B;
-};
 
-template <int NT>
+// PROD != 0: the prefill step, q and gate taken from the projection rows a.qkv
+// (bf16: PROD 1, fp32: PROD 2): each wave builds its q rows in the B-operand
+// layout with the producer's arithmetic (prefill_q_row) and reads the gate
+// from the rows in the epilogue (fp32 rounded to bf16 first, as the producer
+// writes it), so the result has the bits of kvc_qkv_append + the plain
+// kernel.
+template <int NT, int PROD>
 __global__ __launch_bounds__(64 * 8 / NT) __attribute__((amdgpu_waves_per_eu(2 / NT, 2 / NT)))
 void prefill_mfma_kernel(PrefillArgs a) {
+    constexpr bool PRODUCE = PROD != 0;
+    constexpr bool F32IN = PROD == 2;
     constexpr int kWavesPf = 8 / NT;
     constexpr int kRowsPerWave = 16 * NT;
     constexpr int kLoadRows = kPfKeys / kWavesPf;  // tile rows each wave loads
@@ -1324,15 +1464,21 @@ void prefill_mfma_kernel(PrefillArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int r = row0 + min(rw0 + 16 * nt + r16, rows - 1);
-        const uint16_t* qr = a.q + (((size_t)s * a.n_q + r) * kQHeads + h * kGroup + g) * kHeadDim;
+        if constexpr (PRODUCE) {
+            const size_t row = ((size_t)s * a.n_q + r) * kQkvRow + (size_t)(h * kGroup + g) * 2 * kHeadDim;
+            prefill_q_row<F32IN>(a.qkv, row, a.q_norm, a.rope, a.rope_rows, a.rope_half, pos0 + r, a.eps, q4, qflip,
+                                 qb[nt]);
+        } else {
+            const uint16_t* qr = a.q + (((size_t)s * a.n_q + r) * kQHeads + h * kGroup + g) * kHeadDim;
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            u32x4 x = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * q4);
-            x[0] ^= qflip;
-            x[1] ^= qflip;
-            x[2] ^= qflip;
-            x[3] ^= qflip;
-            qb[nt][ks] = as_bf16x8(x);
+            for (int ks = 0; ks < 8; ks++) {
+                u32x4 x = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * q4);
+                x[0] ^= qflip;
+                x[1] ^= qflip;
+                x[2] ^= qflip;
+                x[3] ^= qflip;
+                qb[nt][ks] = as_bf16x8(x);
+            }
         }
     }
 
@@ -1587,8 +1733,20 @@ void prefill_mfma_kernel(PrefillArgs a) {
         for (int dt = 0; dt < 16; dt++) {
             const int d0 = 16 * dt + 4 * q4;
             float v4[4] = {o[dt][nt][0] * inv, o[dt][nt][1] * inv, o[dt][nt][2] * inv, o[dt][nt][3] * inv};
-            if (a.gate) {
-                const uint2 gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+            if (PRODUCE || a.gate) {
+                uint2 gw;
+                if constexpr (PRODUCE) {
+                    const size_t ge = ((size_t)s * a.n_q + row0 + rl) * kQkvRow +
+                                      (size_t)(h * kGroup + g) * 2 * kHeadDim + kHeadDim + d0;
+                    if constexpr (F32IN) {
+                        const float4 f = *reinterpret_cast<const float4*>(static_cast<const float*>(a.qkv) + ge);
+                        gw = make_uint2(cvt_pk_bf16(f.x, f.y), cvt_pk_bf16(f.z, f.w));
+                    } else {
+                        gw = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.qkv) + ge);
+                    }
+                } else {
+                    gw = *reinterpret_cast<const uint2*>(a.gate + orow + d0);
+                }
                 v4[0] *= gate_sigmoid(bf16lo(gw.x), a.gate_ref);
                 v4[1] *= gate_sigmoid(bf16hi(gw.x), a.gate_ref);
                 v4[2] *= gate_sigmoid(bf16lo(gw.y), a.gate_ref);
@@ -1674,6 +1832,9 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
     const int hl = lane & 31, sub = lane >> 5;  // lane in the half, which half
     const int d0 = hl * 8;
     const bool kv_wave = wave == kQkvWaves - 1;  // rows 16..19: the kv heads
+    // with neither q nor gate written out (the prefill step builds q itself)
+    // only the kv wave has work: the q / gate rows are not read
+    if (!kv_wave && !a.q_out && !a.gate_out) return;
     constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
     const int half = a.rope_half;
     const bool roped = d0 < 2 * half;
@@ -3051,7 +3212,13 @@ int launch_checksum(const ChecksumArgs& a, void* stream) {
 
 int launch_prefill(const PrefillArgs& a, void* stream) {
     const int grid = 8 * ((a.n_groups + 7) / 8) * ((a.n_q + kPfRows - 1) / kPfRows);
-    hipLaunchKernelGGL(prefill_mfma_kernel<kPfNT>, dim3(grid), dim3(64 * 8 / kPfNT), 0, (hipStream_t)stream, a);
+    const hipStream_t st = (hipStream_t)stream;
+    if (a.qkv && a.qkv_f32)
+        hipLaunchKernelGGL((prefill_mfma_kernel<kPfNT, 2>), dim3(grid), dim3(64 * 8 / kPfNT), 0, st, a);
+    else if (a.qkv)
+        hipLaunchKernelGGL((prefill_mfma_kernel<kPfNT, 1>), dim3(grid), dim3(64 * 8 / kPfNT), 0, st, a);
+    else
+        hipLaunchKernelGGL((prefill_mfma_kernel<kPfNT, 0>), dim3(grid), dim3(64 * 8 / kPfNT), 0, st, a);
     return (int)hipGetLastError();
 }
 

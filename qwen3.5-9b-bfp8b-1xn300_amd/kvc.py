@@ -43,7 +43,7 @@ EXPORTS = [
     "kvc_get_stats", "kvc_abi_version", "kvc_seq_create", "kvc_seq_release",
     "kvc_seq_reset", "kvc_seq_len", "kvc_seq_truncate", "kvc_seq_reserve",
     "kvc_seq_commit", "kvc_prefix_match", "kvc_append", "kvc_qkv_append", "kvc_decode_attn",
-    "kvc_decode_attn_static", "kvc_decode_step", "kvc_prefill_attn", "kvc_gather", "kvc_kv_checksum", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
+    "kvc_decode_attn_static", "kvc_decode_step", "kvc_prefill_attn", "kvc_prefill_step", "kvc_gather", "kvc_kv_checksum", "kvc_state_ptrs", "kvc_deltanet_step", "kvc_snapshot_save",
     "kvc_snapshot_restore", "kvc_snapshot_release", "kvc_pool_fill_normal",
     "kvc_fill_normal_bf16", "kvc_sync",
 ]
@@ -117,6 +117,7 @@ def lib() -> ctypes.CDLL:
             "kvc_decode_step": (ctypes.c_int, [P, I32, pI32, I32, P, I32, P, P, P, I32, F32, P]),
             "kvc_kv_checksum": (ctypes.c_int, [P, I32, pI32, I32, P, P]),
             "kvc_prefill_attn": (ctypes.c_int, [P, I32, pI32, I32, I32, P, P, P, I32, F32, P]),
+            "kvc_prefill_step": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, I32, F32, P]),
             "kvc_gather": (ctypes.c_int, [P, I32, pI32, I32, I32, pI32, P, P, P]),
             "kvc_state_ptrs": (ctypes.c_int, [P, I32, I32, ctypes.POINTER(P), ctypes.POINTER(P)]),
             "kvc_deltanet_step": (ctypes.c_int, [P, I32, pI32, I32, I32, P, I32, P, P, P, P, P, I32, P]),
@@ -399,6 +400,13 @@ class Context:
                      scale=1.0 / 16, stream=None):
         _check(self.L.kvc_prefill_attn(self.ptr, layer, _i32(seqs), len(seqs), n_q, self._p(q),
                                        self._p(gate), self._p(out), out_dtype, ctypes.c_float(scale), stream))
+
+    def prefill_step(self, layer, seqs, n_q, qkv, q_norm, k_norm, out, in_dtype=DTYPE_BF16, out_dtype=DTYPE_F32,
+                     scale=1.0 / 16, stream=None):
+        """qkv_append (K/V) + gated prefill_attn with q and gate built from the rows"""
+        _check(self.L.kvc_prefill_step(self.ptr, layer, _i32(seqs), len(seqs), n_q, self._p(qkv), in_dtype,
+                                       self._p(q_norm), self._p(k_norm), self._p(out), out_dtype,
+                                       ctypes.c_float(scale), stream))
 
     def gather(self, layer, seqs, tok0, n_tok, k_out, v_out, stream=None):
         _check(self.L.kvc_gather(self.ptr, layer, _i32(seqs), len(seqs), tok0, _i32(n_tok),
