@@ -756,6 +756,16 @@ def run_c(args):
         "gather": lambda: [ctx.gather(l_, sess, 0, lens_, kout, vout, stream) for l_ in range(layers)],
         "prefill": lambda: [ctx.prefill_attn(l_, sess, n_q, qb, ob, out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16,
                                              stream=stream) for l_ in range(layers)],
+        # the whole gated attention step of the chunk from its projection rows:
+        # producer (q, gate, K, V) + prefill, against kvc_prefill_step
+        "step_two_launch": lambda: [
+            (ctx.qkv_append(l_, sess, n_q, qkv, qn, kn_w, q_out=q2, gate_out=g2, in_dtype=kvc.DTYPE_BF16,
+                            stream=stream),
+             ctx.prefill_attn(l_, sess, n_q, q2, ob, gate=g2, out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16,
+                              stream=stream)) for l_ in range(layers)],
+        "step_fused": lambda: [ctx.prefill_step(l_, sess, n_q, qkv, qn, kn_w, ob, in_dtype=kvc.DTYPE_BF16,
+                                                out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
+                               for l_ in range(layers)],
     }
     leg_us = {}
     e0, e1 = h.event(), h.event()
@@ -797,6 +807,12 @@ def run_c(args):
             **ceiling_fields(flops / (p_us * 1e-6) / 1e12),
             "prefill_GBps": round(p_bytes / (p_us * 1e-6) / 1e9, 1),
             **hbm_rate("prefill", p_us, "prefill_traffic_bytes_per_launch"),
+            "attention_step": {
+                "two_launch_us_per_layer": round(leg_us["step_two_launch"], 1),
+                "fused_us_per_layer": round(leg_us["step_fused"], 1),
+                "note": "the gated attention step of the 128-token chunks from their bf16 projection rows per "
+                        "layer: kvc_qkv_append (q, gate, K, V) + kvc_prefill_attn against kvc_prefill_step "
+                        "(K/V side of the producer, then the prefill building q and gate from the rows; same bits)"},
             "mean_prefix": float(P.mean()),
             **({} if args.no_cpu else {"cpu_baseline": cpu_baseline_c(P)})}
 
