@@ -1822,18 +1822,25 @@ constexpr int kQkvWaves = 5;
 // tokens per producer workgroup (all their rows are loaded first); 2 and 4
 // tokens measured no faster than 1
 constexpr int kQkvTok = 1;
-template <bool BF16IN>
+// KVONLY: neither q nor gate is written out (the prefill step builds q
+// itself), so only the k / v rows have work: a 256-thread workgroup takes 4
+// consecutive tokens, one per wave, each wave doing what wave 4 does above
+constexpr int kQkvKvWaves = 4;
+template <bool BF16IN, bool KVONLY>
 __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
 #pragma clang fp contract(off)
-    const int per_seq = (a.n_tok + kQkvTok - 1) / kQkvTok;
+    constexpr int kTokPerWg = KVONLY ? kQkvKvWaves : kQkvTok;
+    const int per_seq = (a.n_tok + kTokPerWg - 1) / kTokPerWg;
     const int s = blockIdx.x / per_seq;
-    const int tok0 = (blockIdx.x - s * per_seq) * kQkvTok;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tok0 = (blockIdx.x - s * per_seq) * kTokPerWg + (KVONLY ? wave : 0);
+    if (KVONLY && tok0 >= a.n_tok) return;  // whole wave
+    const int rw = KVONLY ? kQkvWaves - 1 : wave;  // row group: 4 rw .. 4 rw + 3
     const int hl = lane & 31, sub = lane >> 5;  // lane in the half, which half
     const int d0 = hl * 8;
-    const bool kv_wave = wave == kQkvWaves - 1;  // rows 16..19: the kv heads
-    // with neither q nor gate written out (the prefill step builds q itself)
-    // only the kv wave has work: the q / gate rows are not read
+    const bool kv_wave = rw == kQkvWaves - 1;  // rows 16..19: the kv heads
+    // with neither q nor gate written out only the kv wave has work (the
+    // host launches the KVONLY form then; this keeps the other correct)
     if (!kv_wave && !a.q_out && !a.gate_out) return;
     constexpr size_t kKOff = (size_t)kQHeads * 2 * kHeadDim;  // k rows, then v rows
     const int half = a.rope_half;
@@ -1854,7 +1861,7 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
         const size_t row = ((size_t)s * a.n_tok + tok) * kQkvRow;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int r = wave * 4 + i * 2 + sub;
+            const int r = rw * 4 + i * 2 + sub;
             const size_t xo = kv_wave ? row + kKOff + (size_t)(r - kQHeads) * kHeadDim : row + (size_t)r * 2 * kHeadDim;
             const size_t co = kv_wave ? row + kKOff + (size_t)(kKvHeads + r - kQHeads) * kHeadDim
                                       : row + (size_t)r * 2 * kHeadDim + kHeadDim;
@@ -1904,7 +1911,7 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
         // copied rows: gate heads, or (wave 4) the v heads
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int r = wave * 4 + i * 2 + sub;
+            const int r = rw * 4 + i * 2 + sub;
             if (kv_wave) {
                 const size_t slot =
                     (((size_t)blk * kKvHeads + (r - kQHeads)) * kBlockTok + pos % kBlockTok) * kHeadDim + d0;
@@ -1923,7 +1930,7 @@ __global__ __launch_bounds__(kQkvWaves * 64) void qkv_append_kernel(QkvArgs a) {
         // normalized rows: RMSNorm, RoPE, bf16
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int r = wave * 4 + i * 2 + sub;  // 0..15 q heads, 16..19 k heads
+            const int r = rw * 4 + i * 2 + sub;  // 0..15 q heads, 16..19 k heads
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; j++) ss += x[tt][i][j] * x[tt][i][j];
@@ -3231,11 +3238,19 @@ int launch_append(const AppendArgs& a, void* stream) {
 
 int launch_qkv_append(const QkvArgs& a, void* stream) {
     static_assert(kQkvWaves * 4 == kQHeads + kKvHeads, "two pairs of head rows per wave");
+    if (!a.q_out && !a.gate_out) {  // k / v rows only: one token per wave
+        const dim3 grid(a.n_seqs * ((a.n_tok + kQkvKvWaves - 1) / kQkvKvWaves)), block(kQkvKvWaves * 64);
+        if (a.in_bf16)
+            hipLaunchKernelGGL((qkv_append_kernel<true, true>), grid, block, 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL((qkv_append_kernel<false, true>), grid, block, 0, (hipStream_t)stream, a);
+        return (int)hipGetLastError();
+    }
     const dim3 grid(a.n_seqs * ((a.n_tok + kQkvTok - 1) / kQkvTok)), block(kQkvWaves * 64);
     if (a.in_bf16)
-        hipLaunchKernelGGL(qkv_append_kernel<true>, grid, block, 0, (hipStream_t)stream, a);
+        hipLaunchKernelGGL((qkv_append_kernel<true, false>), grid, block, 0, (hipStream_t)stream, a);
     else
-        hipLaunchKernelGGL(qkv_append_kernel<false>, grid, block, 0, (hipStream_t)stream, a);
+        hipLaunchKernelGGL((qkv_append_kernel<false, false>), grid, block, 0, (hipStream_t)stream, a);
     return (int)hipGetLastError();
 }
 
