@@ -691,7 +691,13 @@ def hbm_rate(leg: str, us: float, key: str):
             f"{leg}_hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 1)}
 
 
-def run_c(args):
+def build_c():
+    """Config c as benched: the context, the 64 sessions with their reused
+    prefixes matched and 128 tokens reserved, the device buffers, and each
+    leg as a function enqueueing its 8 layer launches.  Returns a namespace
+    of all of them; close() frees the buffers and the context."""
+    import types
+
     import kvc
 
     h = kvc.hip()
@@ -746,7 +752,6 @@ def run_c(args):
     # HIP graph of its 8 layer launches, replayed back to back between two
     # events, so neither host enqueue time nor per-launch event records enter
     # the figures.
-    reps = args.c_reps
     lens_ = [int(x) for x in reused]
     legs = {
         "append": lambda: [ctx.append(l_, sess, n_q, kb, vb, stream) for l_ in range(layers)],
@@ -767,6 +772,22 @@ def run_c(args):
                                                 out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
                                for l_ in range(layers)],
     }
+
+    def close():
+        for b_ in (kout, vout, qb, kb, vb, ob, qkv, qn, kn_w, q2, g2):
+            b_.free()
+        ctx.close()
+
+    return types.SimpleNamespace(h=h, ctx=ctx, stream=stream, layers=layers, nses=nses, n_q=n_q, P=P, sess=sess,
+                                 reused=reused, tot_tok=tot_tok, match_us=match_us, qkv_row=qkv_row, qkv=qkv,
+                                 wn=wn, ob=ob, legs=legs, close=close)
+
+
+def run_c(args):
+    C = build_c()
+    h, stream, legs, layers, nses, n_q = C.h, C.stream, C.legs, C.layers, C.nses, C.n_q
+    P, tot_tok, match_us, qkv_row = C.P, C.tot_tok, C.match_us, C.qkv_row
+    reps = args.c_reps
     leg_us = {}
     e0, e1 = h.event(), h.event()
     for name, fn in legs.items():
@@ -787,9 +808,7 @@ def run_c(args):
     g_bytes = 2 * 2 * tot_tok * ROW * 2  # K and V, read + write
     flops = float(sum(16384 * (128 * int(p_) + 8256) for p_ in P))  # causal-exact QK^T + PV
     p_bytes = int(sum(ROW * 2 * 2 * (int(p_) + n_q) for p_ in P)) + 2 * nses * n_q * NQ * D * 2
-    for b_ in (kout, vout, qb, kb, vb, ob, qkv, qn, kn_w, q2, g2):
-        b_.free()
-    ctx.close()
+    C.close()
     return {"workload": "c: 64 sessions, 8 seeded base streams, block-aligned reused prefix U[256,3072] + 128 "
                         "unique tokens; append of the 128 new tokens (plain, and from bf16 projection rows with q/k "
                         "RMSNorm + RoPE), gather of the reused blocks and 128-token causal chunked prefill per layer",
