@@ -86,9 +86,20 @@ __device__ __forceinline__ float schraudolph_exp_rne(float x) {
     return __int_as_float((int)__builtin_rintf(__builtin_fmaf(12102203.0f, x, 1065353216.0f)));
 }
 // The reference's gate sigmoid, fast_sigmoidf (src/engine.cpp:2358-2360):
-// 1 / (1 + fast_expf(-x)) with an IEEE division (hipcc rounds fp32 division
-// correctly by default), bit-exact with that formula for every input but NaN.
-__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + schraudolph_exp(-x)); }
+// 1 / (1 + fast_expf(-x)), correctly rounded as the reference's IEEE division
+// rounds it, bit-exact with that formula for every input but NaN.  With x
+// clamped, y = 1 + fast_expf(-x) lies in [1, 2^127].  Below 2^126 the quotient
+// is v_rcp_f32 (within 1 ulp) followed by one Newton step on FMAs (the
+// residual 1 - y r is exact), which gives the correctly rounded 1 / y for
+// every y the bf16 gates produce (an exhaustive GPU test covers all of them);
+// larger y, whose reciprocal is subnormal, take the full IEEE division
+// sequence (two scalings, five FMAs, a fixup) that the Newton step replaces.
+__device__ __forceinline__ float sigmoid_ref(float x) {
+    const float y = 1.0f + schraudolph_exp(-x);
+    if (__builtin_expect(y >= 0x1p126f, 0)) return 1.0f / y;
+    const float r = __builtin_amdgcn_rcpf(y);
+    return __builtin_fmaf(__builtin_fmaf(-y, r, 1.0f), r, r);
+}
 
 // Raw buffer access with cache-policy bits.  kCpolSC1 marks an access as
 // coherent at agent (device) scope: stores write through the XCD's L2 and
