@@ -198,7 +198,8 @@ int kvc_append(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
  * (cos/sin tables built at kvc_create the way src/engine.cpp:2408-2419 builds
  * them); k and v are appended to layer's cache as bf16 (RNE); q and gate are
  * written as bf16 [n_seqs][n_tok][Hq][D] to q_out / gate_out (either may be
- * NULL), ready for kvc_prefill_attn / kvc_decode_attn. */
+ * NULL), ready for kvc_prefill_attn / kvc_decode_attn.  With both NULL only
+ * the k / v part of each row is read (the K/V side of kvc_prefill_step). */
 int kvc_qkv_append(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
                    int32_t n_seqs, int32_t n_tok, const void* qkv,
                    int32_t in_dtype, const void* q_norm, const void* k_norm,
