@@ -1595,6 +1595,10 @@ void prefill_mfma_kernel(PrefillArgs a) {
             issue_v(t + 1, B ^ 1);
         }
         f32x4 st[4][NT];
+        // the MFMA runs (S here, P.V below) issue at raised wave priority, so
+        // on a SIMD the wave feeding the matrix pipe goes ahead of the other
+        // wave's softmax VALU work
+        __builtin_amdgcn_s_setprio(1);
         compute_s(PfBuf<B>{}, st);
         // pin the pipeline: kPfAhead reads, then (1 read, NT MFMAs) per step
         __builtin_amdgcn_sched_group_barrier(kSgDsRead, kPfAhead, 0);
@@ -1603,6 +1607,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
             if (i + kPfAhead < 32) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 1, 0);
             __builtin_amdgcn_sched_group_barrier(kSgMfma, NT, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
 
         // Tile max in the log2 domain.  A full tile (all keys exist and
         // precede the wave's first row) keeps raw scores: the max is scaled
@@ -1690,6 +1695,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
             w[3] = hi[1];
             vf[i % kPfAhead] = as_bf16x8(w);
         };
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int i = 0; i < kPfAhead; i++) read_vfrag(i);
 #pragma unroll
@@ -1712,6 +1718,7 @@ void prefill_mfma_kernel(PrefillArgs a) {
             if (i + kPfAhead < 32) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 1);
             __builtin_amdgcn_sched_group_barrier(kSgMfma, NT, 1);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     issue_k(0, 0);
