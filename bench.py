@@ -771,6 +771,9 @@ def build_c():
         "step_fused": lambda: [ctx.prefill_step(l_, sess, n_q, qkv, qn, kn_w, ob, in_dtype=kvc.DTYPE_BF16,
                                                 out_dtype=kvc.DTYPE_BF16, scale=1.0 / 16, stream=stream)
                                for l_ in range(layers)],
+        # the K/V side of kvc_prefill_step alone (no q / gate outputs)
+        "step_kv_side": lambda: [ctx.qkv_append(l_, sess, n_q, qkv, qn, kn_w, q_out=None, gate_out=None,
+                                                in_dtype=kvc.DTYPE_BF16, stream=stream) for l_ in range(layers)],
     }
 
     def close():
@@ -792,7 +795,7 @@ def run_c(args):
     e0, e1 = h.event(), h.event()
     for name, fn in legs.items():
         g_ = h.capture(stream, fn)
-        n_rep = reps * (10 if name in ("append", "qkv_append") else 1)
+        n_rep = reps * (10 if name in ("append", "qkv_append", "step_kv_side") else 1)
         h.graph_launch(g_, stream)  # warm-up
         h.record(e0, stream)
         for _ in range(n_rep):
@@ -829,9 +832,13 @@ def run_c(args):
             "attention_step": {
                 "two_launch_us_per_layer": round(leg_us["step_two_launch"], 1),
                 "fused_us_per_layer": round(leg_us["step_fused"], 1),
+                "kv_side_us_per_layer": round(leg_us["step_kv_side"], 1),
+                "kv_side_GBps": round(2 * nses * n_q * ROW * 2 * 2 / (leg_us["step_kv_side"] * 1e-6) / 1e9, 1),
                 "note": "the gated attention step of the 128-token chunks from their bf16 projection rows per "
                         "layer: kvc_qkv_append (q, gate, K, V) + kvc_prefill_attn against kvc_prefill_step "
-                        "(K/V side of the producer, then the prefill building q and gate from the rows; same bits)"},
+                        "(K/V side of the producer, then the prefill building q and gate from the rows; same bits); "
+                        "kv_side: the first of those two launches alone, 4 KiB of each row read and 4 KiB of "
+                        "K/V written per token"},
             "mean_prefix": float(P.mean()),
             **({} if args.no_cpu else {"cpu_baseline": cpu_baseline_c(P)})}
 
