@@ -156,14 +156,19 @@ class DecodeB:
         if h.device_count() < 1:
             raise RuntimeError("no HIP device visible")
         self.L, self.layers, self.reps = L, layers, reps
+        self.retired = []  # graph execs replaced by set_mode, destroyed by close()
+        log(f"b setup [{mode}]: kvc_create")
         ctx = self.ctx = kvc.Context(n_attn_layers=layers, n_ssm_layers=0, max_seqs=max(reps, 4),
                                      max_seq_len=L + 64, pool_blocks=reps * (L // BT + 2), snapshot_slots=0,
                                      alloc_seed=SEED + 2, decode_chunk_blocks=chunk_blocks)
         stream = self.stream = h.stream()
+        log(f"b setup [{mode}]: pool fill")
         ctx.pool_fill_normal(SEED + 2, stream)
+        log(f"b setup [{mode}]: sequences")
         seqs = self.seqs = [ctx.seq_create() for _ in range(reps)]
         ctx.reserve(seqs, L - 1, stream)
         ctx.commit(seqs, L - 1, None, stream)
+        log(f"b setup [{mode}]: buffers")
         n = reps * layers
         self.q = h.malloc(n * NQ * D * 2)
         self.kn = h.malloc(n * ROW * 2)
@@ -184,11 +189,14 @@ class DecodeB:
         self.k_norm = h.malloc(D * 4).upload(rng.uniform(0.5, 1.5, D).astype(np.float32))
         h.stream_sync(stream)
         ctx.reserve(seqs, 1, stream)
+        log(f"b setup [{mode}]: step graphs")
         self.graph = h.capture(stream, lambda: [self.enqueue_step(r) for r in range(reps)])
         self.single = [h.capture(stream, lambda r=r: self.enqueue_step(r)) for r in range(reps)]
         # the read floor: the same replicas' K/V read once per layer by the
         # checksum kernel (whole blocks, no arithmetic to speak of)
+        log(f"b setup [{mode}]: floor graph")
         self.floor_graph = h.capture(stream, lambda: [self.enqueue_floor(r) for r in range(reps)])
+        log(f"b setup [{mode}]: done")
         ctx.commit(seqs, 1, None, stream)
         for s_ in seqs:
             ctx.seq_truncate(s_, L - 1)
@@ -219,8 +227,10 @@ class DecodeB:
         if mode not in self.STEP_MODES:
             raise ValueError(f"mode must be one of {self.STEP_MODES}")
         h, stream, reps = self.h, self.stream, self.reps
-        for g_ in [self.graph] + self.single:
-            h.graph_destroy(g_)
+        # the replaced graph execs stay alive until close(): no graph is
+        # destroyed while the process goes on launching work
+        self.retired += [self.graph] + self.single
+        log(f"b set_mode [{mode}]: step graphs")
         self.mode = mode
         self.ctx.reserve(self.seqs, 1, stream)
         self.graph = h.capture(stream, lambda: [self.enqueue_step(r) for r in range(reps)])
@@ -262,67 +272,91 @@ class DecodeB:
         self.end_round()
 
     def close(self):
-        for g_ in [self.graph, self.floor_graph] + self.single:
+        self.h.stream_sync(self.stream)
+        for g_ in [self.graph, self.floor_graph] + self.single + self.retired:
             self.h.graph_destroy(g_)
         for b_ in (self.q, self.kn, self.vn, self.out, self.gate, self.sums, self.qkv, self.q_norm, self.k_norm):
             b_.free()
         self.ctx.close()
 
 
+B_LEGS = ("decode", "floor", "two_launch", "fused")
+
+
 def run_b(args):
+    """Config b's legs in one process: the headline decode launch, the read
+    floor and the two attention-step modes (--b-legs picks a subset; the
+    first leg's graphs are captured at setup, so a run of one step mode
+    alone never re-captures)."""
     L, layers = 4096, 8
-    log(f"config b: {layers} layers, L={L}, {args.replicas} replicas, pool fill")
-    B = DecodeB(reps=args.replicas, chunk_blocks=args.chunk_blocks, L=L, layers=layers)
-    h, stream, run_steps, reps = B.h, B.stream, B.run_steps, B.reps
+    legs = [x for x in args.b_legs.split(",") if x]
+    if not legs or set(legs) - set(B_LEGS):
+        raise SystemExit(f"--b-legs takes a comma list of {B_LEGS} (got {args.b_legs!r})")
+    modes = [m for m in ("decode", "two_launch", "fused") if m in legs]
+    log(f"config b: {layers} layers, L={L}, {args.replicas} replicas, legs {','.join(legs)}")
+    B = DecodeB(reps=args.replicas, chunk_blocks=args.chunk_blocks, L=L, layers=layers,
+                mode=modes[0] if modes else "decode")
+    h, stream, reps = B.h, B.stream, B.reps
     steps = args.steps
-    run_steps(args.warmup)
-    h.stream_sync(stream)
     e0, e1 = h.event(), h.event()
-    h.record(e0, stream)
-    t0 = time.perf_counter()
-    run_steps(steps)
-    h.record(e1, stream)
-    ms = h.elapsed_ms(e0, e1)
-    wall = time.perf_counter() - t0
-    us_layer = ms * 1e3 / (steps * layers)
+    step_ms, step_wall = {}, {}
+    for mode in modes:
+        if B.mode != mode:
+            B.set_mode(mode)
+        log(f"b leg {mode}: {args.warmup} + {steps} steps")
+        B.run_steps(args.warmup)
+        h.stream_sync(stream)
+        h.record(e0, stream)
+        t0 = time.perf_counter()
+        B.run_steps(steps)
+        h.record(e1, stream)
+        step_ms[mode] = h.elapsed_ms(e0, e1)
+        step_wall[mode] = time.perf_counter() - t0
     bpl = bytes_per_layer_b(L)
-    gbs = bpl / (us_layer * 1e-6) / 1e9
+    ms = step_ms.get("decode")
+    us_layer = ms * 1e3 / (steps * layers) if ms is not None else None
+    gbs = bpl / (us_layer * 1e-6) / 1e9 if us_layer else None
+    wall = step_wall.get("decode")
 
     # The timed region replays a graph that holds only decode launches, so the
     # decode kernel's average launch duration is the event-timed region over
     # its launches (inter-launch gaps included, so it is an upper bound on the
     # rocprofv3 kernel-trace average of the same command).
     kern_us = us_layer
-    achieved = bpl / (kern_us * 1e-6) / 1e9
+    achieved = gbs
     # single-launch read floor: the checksum kernel reads the same 16 MiB of
     # K/V per layer through the block table, in the same rotated graph setup
-    f_rounds = max(1, steps // (B.reps * 4))
-    B.run_floor(2)
-    h.stream_sync(stream)
-    h.record(e0, stream)
-    B.run_floor(f_rounds)
-    h.record(e1, stream)
-    floor_us = h.elapsed_ms(e0, e1) * 1e3 / (f_rounds * B.reps * layers)
-    # the whole attention step from the projection row, two launches against one
-    step_us = {}
-    for mode in ("two_launch", "fused"):
-        B.set_mode(mode)
-        B.run_steps(args.warmup)
+    floor_us = None
+    if "floor" in legs:
+        log("b leg floor")
+        f_rounds = max(1, steps // (B.reps * 4))
+        B.run_floor(2)
         h.stream_sync(stream)
         h.record(e0, stream)
-        B.run_steps(steps)
+        B.run_floor(f_rounds)
         h.record(e1, stream)
-        step_us[mode] = h.elapsed_ms(e0, e1) * 1e3 / (steps * layers)
+        floor_us = h.elapsed_ms(e0, e1) * 1e3 / (f_rounds * B.reps * layers)
+    # the whole attention step from the projection row, two launches against one
+    step_us = {m: step_ms[m] * 1e3 / (steps * layers) if m in step_ms else None for m in ("two_launch", "fused")}
+    log("b close")
     B.close()
+    sweep = None
+    floor_checksum_us = floor_us
+    if "floor" in legs:
+        log("b leg floor sweep (libkvc_calib.so)")
+        sweep = read_floor_sweep()
+        if sweep is not None:
+            floor_us = min(floor_us, sweep["best"]["us"])
+    rnd = (lambda x, n: None if x is None else round(x, n))
 
     line = {
         "metric": METRIC,
-        "value": round(gbs, 1),
+        "value": rnd(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms / steps, 5),
+        "ms_per_step": rnd(ms / steps if ms is not None else None, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -332,27 +366,31 @@ def run_b(args):
                                "head_dim 256, bf16 cache at 4096 tokens, fused 1-token append + gated GQA "
                                "decode per layer, HIP-graph replay, 4 rotated cache replicas (512 MiB)",
                    "layers": layers, "ctx": L, "replicas": reps},
-        "us_per_layer": round(us_layer, 3),
-        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "us_per_layer": rnd(us_layer, 3),
+        "pct_hbm_peak": rnd(100 * gbs / HBM_PEAK_GBS if gbs else None, 1),
         "bytes_per_layer": bpl,
-        "floor_us": round(floor_us, 3),
-        "floor_note": "one checksum_kernel launch reading the same 16 MiB of K/V (whole blocks) per layer, "
-                      "same graph and replica rotation: the single-launch read floor",
-        "pct_of_floor": round(100 * floor_us / us_layer, 1),
+        "floor_us": rnd(floor_us, 3),
+        "floor_note": "the fastest read-only launch of the same 16 MiB per layer in the same graph and replica "
+                      "rotation: kvc_kv_checksum over the replicas' K/V (floor_checksum_us) and the launch-shape "
+                      "sweep of libkvc_calib.so (floor_sweep: workgroups per CU, loads in flight per lane, "
+                      "contiguous or strided 16-KiB units, plain or non-temporal loads)",
+        "floor_checksum_us": rnd(floor_checksum_us, 3),
+        "floor_sweep": sweep,
+        "pct_of_floor": rnd(100 * floor_us / us_layer if floor_us and us_layer else None, 1),
         "attention_step": {
-            "two_launch_us_per_layer": round(step_us["two_launch"], 3),
-            "fused_us_per_layer": round(step_us["fused"], 3),
+            "two_launch_us_per_layer": rnd(step_us["two_launch"], 3),
+            "fused_us_per_layer": rnd(step_us["fused"], 3),
             "note": "the whole attention step of a decode token from its bf16 projection row (q/k RMSNorm + "
                     "partial RoPE, k/v append, gated decode) per layer, same graph setup: kvc_qkv_append + "
                     "kvc_decode_attn (two launches; the decode walks the appended key) against "
                     "kvc_decode_step (one launch; it folds the new key in after the walk, as "
                     "kvc_decode_attn does with k_new / v_new, and matches that bit for bit)"},
-        "host_wall_us_per_step": round(wall * 1e6 / steps, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "host_wall_us_per_step": rnd(wall * 1e6 / steps if wall is not None else None, 2),
+        "roofline": {"bound": "hbm", "achieved": rnd(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": rnd(achieved / HBM_PEAK_GBS if achieved else None, 4),
                      "traffic": profiled_traffic("decode_kernel_b_ctx4096.txt"),
                      "traffic_source": "profiles/decode_kernel_b_ctx4096.txt (rocprofv3 --pmc, calibrated)",
-                     "kernel": "decode_kernel<2>", "kernel_avg_us": round(kern_us, 3)},
+                     "kernel": "decode_kernel<2>", "kernel_avg_us": rnd(kern_us, 3)},
     }
     if not args.no_cpu:
         res, cores = cpu_baseline_b(L, budget_s=args.cpu_seconds)
@@ -649,6 +687,39 @@ def run_d(args):
 # ---------------------------------------------------------------------------
 # config c: multi-turn prefix reuse, 64 sessions, 128-token chunked prefill
 
+def read_floor_sweep(rounds=25):
+    """The single-launch read floor of config b, swept over launch shapes with
+    libkvc_calib.so: a read-only launch of 16 MiB (128 blocks of K and of V,
+    64 KiB each, at permuted block ids) in config b's graph of 32 launches
+    (4 replicas x 8 layers, 512 MiB in all), for every workgroup count (1, 2,
+    4 or 8 per CU), 16-B loads in flight per lane (2 to 16), contiguous or
+    16-KiB-unit-strided ranges and plain or non-temporal loads that tile the
+    launch.  Returns the table and the fastest shape."""
+    import ctypes
+
+    path = ROOT / "qwen3.5-9b-bfp8b-1xn300_amd" / "libkvc_calib.so"
+    if not path.exists():
+        return None
+    lib = ctypes.CDLL(str(path))
+    lib.kvc_calib_read_floor.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_double)]
+    rows = []
+    for grid in (256, 512, 1024, 2048):
+        for loads in (2, 4, 8, 16):
+            for strided in (0, 1):
+                for nt in (0, 1):
+                    out = ctypes.c_double(0.0)
+                    rc = lib.kvc_calib_read_floor(grid, loads, strided, nt, rounds, ctypes.byref(out))
+                    if rc == 1:  # hipErrorInvalidValue: the shape does not tile 16 MiB
+                        continue
+                    if rc != 0:
+                        raise RuntimeError(f"kvc_calib_read_floor({grid}, {loads}, {strided}, {nt}): HIP error {rc}")
+                    rows.append({"workgroups_per_cu": grid // 256, "loads_per_lane": loads,
+                                 "bytes_per_workgroup": (16 << 20) // grid, "strided_units": bool(strided),
+                                 "nontemporal": bool(nt), "us": round(out.value, 3)})
+    best = min(rows, key=lambda r: r["us"])
+    return {"shapes": rows, "best": best}
+
+
 def mfma_data_ceiling():
     """The dense bf16 MFMA rate the prefill's operand data allows, measured
     on this GPU with libkvc_calib.so: an MFMA-only v_mfma_f32_32x32x16_bf16
@@ -833,7 +904,11 @@ def run_c(args):
                 "two_launch_us_per_layer": round(leg_us["step_two_launch"], 1),
                 "fused_us_per_layer": round(leg_us["step_fused"], 1),
                 "kv_side_us_per_layer": round(leg_us["step_kv_side"], 1),
-                "kv_side_GBps": round(2 * nses * n_q * ROW * 2 * 2 / (leg_us["step_kv_side"] * 1e-6) / 1e9, 1),
+                # algorithmic bytes over time, not an HBM rate: the 8 layer
+                # launches read the same 33.5 MB of k / v rows, which the
+                # 256 MB Infinity Cache can hold between them
+                "kv_side_algorithmic_GBps": round(2 * nses * n_q * ROW * 2 * 2 / (leg_us["step_kv_side"] * 1e-6) / 1e9,
+                                                  1),
                 "note": "the gated attention step of the 128-token chunks from their bf16 projection rows per "
                         "layer: kvc_qkv_append (q, gate, K, V) + kvc_prefill_attn against kvc_prefill_step "
                         "(K/V side of the producer, then the prefill building q and gate from the rows; same bits); "
@@ -1090,6 +1165,9 @@ def main():
     ap.add_argument("--e-reps", type=int, default=3)
     ap.add_argument("--replicas", type=int, default=4)
     ap.add_argument("--chunk-blocks", type=int, default=0)
+    ap.add_argument("--b-legs", default=",".join(B_LEGS),
+                    help="config b: comma list of the legs to run (decode = the headline launch, floor, "
+                         "two_launch, fused = the attention step modes)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--phases", action="store_true",

@@ -86,7 +86,10 @@ enum { KVC_DTYPE_F32 = 0, KVC_DTYPE_BF16 = 1 };
 /* Transcendentals.  By default the library computes the reference's
  * Schraudolph (1999) approximations (src/engine.cpp:2349-2376): the output
  * gate sigma(gate) of decode and prefill attention (:3563, :2923), bit-exact
- * with fast_sigmoidf for every bf16 gate value, and in the Gated-DeltaNet
+ * for every bf16 gate value with fast_sigmoidf evaluated with an IEEE
+ * division (the reference's fast-math build vectorises that loop with an
+ * approximate reciprocal plus one Newton step, which can differ from the
+ * IEEE quotient by 1 ulp), and in the Gated-DeltaNet
  * step the SiLU of the conv output and of z, the beta sigmoid and the exp in
  * softplus (:2626, :2671, :2674, :2714).  This flag selects exact functions
  * instead (hardware exp/log/rcp, within 2 ulp). */
@@ -224,7 +227,8 @@ int kvc_decode_attn(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
  * the context's.  The call allocates nothing.  A launch needing more than
  * 4096 items (chunks x kv heads x output-dim parts) is refused with
  * KVC_ERR_RANGE before anything runs; the automatic split (decode_chunk_blocks
- * = 0) never needs more, for 64 sequences of any length.  Every call on one GPU shares
+ * = 0) never needs more, for 64 sequences of any length, with or without a
+ * forced output-dim split (KVC_FLAG_DECODE_SPLIT_D).  Every call on one GPU shares
  * that workspace: calls that overlap on one GPU (other streams, other
  * contexts, other host threads) race and must be serialised by the caller. */
 int kvc_decode_attn_static(kvc_ctx* ctx, int32_t layer, const int32_t* seqs,
@@ -300,9 +304,16 @@ int kvc_state_ptrs(kvc_ctx* ctx, int32_t seq, int32_t ssm_layer, void** rec,
  * first, tap 3 on the input), dt_bias [v_heads], a [v_heads] (decay =
  * exp(softplus(alpha + dt_bias) * a)), norm_w [v_dim].  out: [n_seqs][n_tok]
  * [v_heads * v_dim], fp32 or bf16 (RNE) by out_dtype: the gated-RMSNorm
- * output (o / rms(o) * norm_w * silu(z), o = S q / 11.3137).  exp, log,
- * sigmoid and SiLU use the hardware exp2/log2/reciprocal (each within 2 ulp)
- * where the reference uses Schraudolph approximations (:2349-2374).  Built for
+ * output (o / rms(o) * norm_w * silu(z), o = S q / 11.3137).  By default the
+ * SiLU of the conv output and of z, the beta sigmoid and the exp inside
+ * softplus are the reference's Schraudolph forms (:2349-2374, :2626, :2671,
+ * :2674, :2714); beta's division is correctly rounded, as the reference's
+ * scalar fast_sigmoidf divides, and the SiLU's reciprocal is v_rcp_f32
+ * (1 ulp), as the reference's fast-math AVX-512 SiLU takes an approximate
+ * reciprocal.  The decay's exp and the softplus log are the hardware
+ * exp2/log2 (within 2 ulp of libm's expf / logf).  With KVC_FLAG_EXACT_MATH
+ * the SiLU, sigmoid and softplus use the hardware exp2/log2/reciprocal
+ * (each within 2 ulp of the exact function) instead.  Built for
  * 32 v-heads, 16 k-heads, 128 x 128 heads, a 3-row window and 8192 channels
  * (KVC_ERR_UNSUPPORTED otherwise); one seq's n_tok rows of proj must span
  * less than 2 GiB (KVC_ERR_RANGE otherwise). */

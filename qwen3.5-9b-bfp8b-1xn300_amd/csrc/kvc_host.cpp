@@ -1143,9 +1143,11 @@ static int build_decode_args(kvc_ctx* c, int32_t layer, const int32_t* seqs, int
         }
         // an automatic chunk also grows until the launch has at most
         // kAutoItems items (each sequence's last, partial chunk adds one per
-        // kv head), the same in either workspace; a chunk size the caller set
-        // is kept and checked below
-        if (total_chunks <= max_chunks && (!auto_cb || total_chunks * kKvHeads <= kAutoItems)) break;
+        // kv head, and a forced output-dim split doubles them), the same in
+        // either workspace; a chunk size the caller set is kept and checked
+        // below
+        const int64_t auto_items = total_chunks * kKvHeads * (force_split ? kMaxDParts : 1);
+        if (total_chunks <= max_chunks && (!auto_cb || auto_items <= kAutoItems)) break;
         cb *= 2;
     }
     int32_t d_parts = 1;

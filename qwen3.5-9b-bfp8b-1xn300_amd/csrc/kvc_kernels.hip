@@ -2043,9 +2043,11 @@ __device__ __forceinline__ float raw_f(uint32_t r) {
 }
 
 // Gated-DeltaNet transcendentals on the hardware units (v_exp_f32, v_log_f32,
-// v_rcp_f32, v_rsq_f32; each within 2 ulp of the exact value, where the
-// reference uses Schraudolph's approximations).  Every DeltaNet kernel uses
-// these, so a token gives the same bits through any of them.
+// v_rcp_f32, v_rsq_f32; each within 2 ulp of the exact value).  The decay's
+// exp, the softplus log and the norms' rsqrt always use them; the sigmoid and
+// SiLU below use them only with KVC_FLAG_EXACT_MATH (REF = false).  Every
+// DeltaNet kernel shares these helpers, so a token gives the same bits
+// through any of them.
 __device__ __forceinline__ float dn_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 __device__ __forceinline__ float dn_log(float x) { return __builtin_amdgcn_logf(x) * 0.6931471805599453f; }
 __device__ __forceinline__ float dn_rsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
@@ -2054,16 +2056,18 @@ __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 
 // Reference math (REF, the default; KVC_FLAG_EXACT_MATH clears it): the
 // reference's Schraudolph forms.  beta = fast_sigmoidf(beta_raw) (scalar exp,
-// truncating conversion, src/engine.cpp:2674 / :3281); SiLU of the conv
-// output and of z is the AVX-512 form (exp converted to nearest even,
-// :2626, :2714, :3227, :3321); softplus takes log(1 + fast_expf(b)) (:2671,
-// :3278).  The reciprocal is v_rcp_f32 (1 ulp): the reference's fast-math
-// build computes x / (1 + e) with an approximate reciprocal too, so no exact
-// bits exist to match there; the bound is tested against the oracle.
+// truncating conversion, src/engine.cpp:2674 / :3281): the reference's
+// scalar division is an IEEE divide even in its fast-math build, so beta
+// takes the correctly rounded quotient of sigmoid_ref and matches it bit for
+// bit.  SiLU of the conv output and of z is the AVX-512 form (exp converted
+// to nearest even, :2626, :2714, :3227, :3321), whose fast-math build divides
+// by an approximate reciprocal: here v_rcp_f32 (1 ulp), so no exact bits
+// exist to match there and the bound is tested against the oracle.  softplus
+// takes log(1 + fast_expf(b)) (:2671, :3278).
 template <bool REF>
-__device__ __forceinline__ float dn_sigmoid(float x) {
+__device__ __forceinline__ float dn_beta(float x) {
     if constexpr (REF)
-        return __builtin_amdgcn_rcpf(1.0f + schraudolph_exp(-x));
+        return sigmoid_ref(x);
     else
         return sigmoid_f(x);
 }
@@ -2145,7 +2149,7 @@ __device__ __forceinline__ void dn_gates(float alpha, float braw, float dtb, flo
     const float ex = REF ? schraudolph_exp(biased) : dn_exp(biased);
     const float sp = biased > 20.0f ? biased : dn_log(1.0f + ex);
     decay = dn_exp(sp * av);
-    beta = dn_sigmoid<REF>(braw);
+    beta = dn_beta<REF>(braw);
 }
 
 // gated RMSNorm of one v-head's 128 outputs (o_row) and the store of dims
@@ -2690,7 +2694,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 const float ex = REF ? schraudolph_exp(biased) : dn_exp(biased);
                 const float sp = biased > 20.0f ? biased : dn_log(1.0f + ex);
                 l_a = sp * a_g;
-                be = dn_sigmoid<REF>(raw_f<BF16IN>(braw_n));
+                be = dn_beta<REF>(raw_f<BF16IN>(braw_n));
             }
             lg[q % 3][ab_h][ab_t] = l_a;
             bt[q % 3][ab_h][ab_t] = be;

@@ -47,7 +47,9 @@ struct kvc_ctx;
 
 namespace kvengine {
 
-enum StopReason { STOP_LENGTH = 0, STOP_EOS = 1, STOP_CALLBACK = 2 };
+// Same enumerators and values as the reference (src/engine.h:23): a caller
+// that stores or compares the numeric value sees the same codes.
+enum StopReason { STOP_EOS = 0, STOP_LENGTH = 1, STOP_CALLBACK = 2 };
 
 using TokenCallback = std::function<bool(int token_id, const std::string& text)>;
 

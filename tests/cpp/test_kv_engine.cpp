@@ -20,6 +20,11 @@
 #include "../../include/kvc.h"
 #include "../../qwen3.5-9b-bfp8b-1xn300_amd/engine/kv_engine.h"
 
+// The stop reasons carry the reference's numeric values (src/engine.h:23:
+// enum StopReason { STOP_EOS, STOP_LENGTH, STOP_CALLBACK }).
+static_assert(kvengine::STOP_EOS == 0 && kvengine::STOP_LENGTH == 1 && kvengine::STOP_CALLBACK == 2,
+              "StopReason values differ from the reference's engine.h");
+
 // ---- checks ----------------------------------------------------------------
 // Each check is counted; a failed one prints where and what was compared, and
 // the run continues so that one report lists every failure.

@@ -31,3 +31,10 @@ def test_config_a_runs_on_the_host_and_prints_one_json_line():
     assert a["prefix_reuse"] == 512  # the 512-token cached prefix is matched
     assert a["finite"] is True
     assert a["decode_ms_1thread"] > 0 and a["append_us"] > 0 and a["prefix_match_us"] > 0
+
+
+def test_config_b_legs_are_checked_before_any_gpu_work():
+    r = run("--config", "b", "--b-legs", "decode,bogus", timeout=120)
+    assert r.returncode != 0
+    assert "--b-legs takes a comma list" in (r.stdout + r.stderr)
+    assert not r.stdout.strip().startswith("{")

@@ -176,3 +176,43 @@ def test_kv_checksum_definition():
     assert np.array_equal(c2[1:], c[1:])
     k3 = np.concatenate([k, np.full((1, 4, 256), 7, np.uint16)])[:L]  # nothing past L is read
     assert np.array_equal(O.kv_checksums(k3, v), c)
+
+
+def _ulp32(v: float) -> "O.Fraction":
+    """Spacing of fp32 values at |v| (normal range)."""
+    e = math.frexp(abs(v))[1] - 1
+    return O.Fraction(2) ** (max(e, -126) - 23)
+
+
+def test_gate_reciprocal_estimate_plus_newton_within_one_ulp():
+    """The reference is built with clang -ffast-math (Makefile:14, :47), which
+    vectorises the gate loop (src/engine.cpp:2923, :3563) and divides there by
+    vrcp14ps (relative error below 2^-14) refined by one Newton step on FMAs:
+    r1 = fma(r0, fma(-y, r0, 1), r0).  The library's gate (and the oracle's
+    model) is the correctly rounded quotient 1 / y.  For every y the bf16
+    gates produce and for estimates r0 anywhere inside the rcp14 error bound,
+    r1 lies within 1 ulp of that quotient: the two agree to 1 ulp of sigma,
+    whatever table the hardware estimate uses.  Exact rational arithmetic;
+    each FMA rounds once."""
+    F = O.Fraction
+    L = O.L()
+    one = np.float32(1.0)
+    ys = sorted({float(one + np.float32(L.orc_fast_expf(-x))) for x in O.finite_bf16_values().tolist()})
+    ys = [y for y in ys if y < 2.0 ** 126]  # 1 / y normal
+    eps = [F(-1, 2 ** 14) * F(1023, 1024), F(-1, 2 ** 16), F(0), F(1, 2 ** 17), F(1, 2 ** 14) * F(1023, 1024)]
+    worst = F(0)
+    differ = 0
+    for i, y in enumerate(ys):
+        fy = F(y)
+        exact = O.f32_round(1 / fy)
+        ulp = _ulp32(exact)
+        for e in (eps if i % 8 == 0 else eps[::4]):
+            r0 = F(O.f32_round(F(1) / fy * (1 + e)))
+            t = F(O.f32_round(1 - fy * r0))      # fma(-y, r0, 1)
+            r1 = O.f32_round(r0 * t + r0)         # fma(r0, t, r0)
+            d = abs(F(r1) - F(exact)) / ulp
+            worst = max(worst, d)
+            differ += r1 != exact
+    assert worst <= 1, float(worst)
+    # the bound is not vacuous: some estimates do land 1 ulp away
+    assert differ > 0

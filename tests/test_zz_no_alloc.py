@@ -156,3 +156,88 @@ def test_static_decode_auto_split_large_batch():
         assert np.isfinite(O.bf16_to_f32(a)).all()
         for b_ in (q, gate, o1, o2):
             b_.free()
+
+
+def test_static_decode_forced_split_auto_chunk_fits():
+    """With the output-dim split forced on, the automatic chunk counts both
+    parts against the 4096-item cap, so a batch that would need 8192 items at
+    the uncapped chunk (16 x 16384 tokens) still fits the static array and
+    equals the regular call bit for bit."""
+    say("static vs regular decode, forced output-dim split, automatic chunk, 16 x 16384 tokens")
+    h = kvc.hip()
+    n, L = 16, 16384
+    with kvc.Context(n_attn_layers=1, n_ssm_layers=0, max_seqs=n, max_seq_len=L, pool_blocks=n * L // 32 + 16,
+                     snapshot_slots=0, alloc_seed=85, flags=kvc.FLAG_DECODE_SPLIT_D) as ctx:
+        ctx.pool_fill_normal(86)
+        seqs = [ctx.seq_create() for _ in range(n)]
+        ctx.reserve(seqs, L)
+        ctx.commit(seqs, L)
+        q = kvc.to_device(O.normal_bf16(n * NQ * D, 87))
+        o1, o2 = h.malloc(n * NQ * D * 4), h.malloc(n * NQ * D * 4)
+        rc = call_static(ctx, 0, seqs, q, o2)
+        assert rc == kvc.KVC_OK, kvc.lib().kvc_last_error()
+        ctx.decode_attn(0, seqs, q, o1)
+        ctx.sync()
+        a, b = o1.download(np.uint32, (n, NQ, D)), o2.download(np.uint32, (n, NQ, D))
+        assert np.array_equal(a, b)
+        assert np.isfinite(a.view(np.float32)).all()
+        for b_ in (q, o1, o2):
+            b_.free()
+
+
+def test_static_decode_allocates_nothing_and_replays_from_a_graph():
+    """The property the entry point exists for.  Once the context exists, a
+    static call leaves the device's free memory unchanged, and the call
+    captured into a HIP graph replays correctly: three replays, with eager
+    decodes and synchronisations between them, each equal bit for bit to the
+    regular call on the same inputs."""
+    say("static decode: free memory unchanged across a call; captured into a HIP graph, three replays")
+    h = kvc.hip()
+    n, L = 4, 5000
+    with kvc.Context(n_attn_layers=1, n_ssm_layers=0, max_seqs=n, max_seq_len=8192, pool_blocks=n * 160,
+                     snapshot_slots=0, alloc_seed=88) as ctx:
+        ctx.pool_fill_normal(89)
+        seqs = [ctx.seq_create() for _ in range(n)]
+        ctx.reserve(seqs, L)
+        ctx.commit(seqs, L)
+        q = kvc.to_device(O.normal_bf16(n * NQ * D, 90))
+        gate = kvc.to_device(O.normal_bf16(n * NQ * D, 91))
+        o_ref, o_st = h.malloc(n * NQ * D * 2), h.malloc(n * NQ * D * 2)
+        ctx.decode_attn(0, seqs, q, o_ref, gate=gate, out_dtype=kvc.DTYPE_BF16)
+        ctx.sync()
+        want = o_ref.download(np.uint16, (n, NQ, D))
+        # the first static call on this device already happened at create:
+        # a call now must not change the free memory
+        rc = call_static(ctx, 0, seqs, q, o_st, gate=gate, out_dtype=kvc.DTYPE_BF16)
+        assert rc == kvc.KVC_OK, kvc.lib().kvc_last_error()
+        ctx.sync()
+        free0, _ = h.mem_info()
+        rc = call_static(ctx, 0, seqs, q, o_st, gate=gate, out_dtype=kvc.DTYPE_BF16)
+        assert rc == kvc.KVC_OK, kvc.lib().kvc_last_error()
+        ctx.sync()
+        free1, _ = h.mem_info()
+        assert free1 == free0, (free0, free1)
+        assert np.array_equal(o_st.download(np.uint16, (n, NQ, D)), want)
+        # capture on a stream of our own, then replay
+        stream = h.stream()
+        rcs = []
+        graph = h.capture(stream, lambda: rcs.append(
+            static_fn()(ctx.ptr, 0, ctypes.cast((ctypes.c_int32 * n)(*seqs), ctypes.c_void_p), n, q.ptr, None,
+                        None, gate.ptr, o_st.ptr, kvc.DTYPE_BF16, ctypes.c_float(1.0 / 16), stream)))
+        assert rcs == [kvc.KVC_OK], kvc.lib().kvc_last_error()
+        try:
+            for rep in range(3):
+                h.L.hipMemset(o_st.ptr, 0xFF, n * NQ * D * 2)  # poison: a replay that writes nothing fails
+                h.sync()
+                h.graph_launch(graph, stream)
+                h.stream_sync(stream)
+                got = o_st.download(np.uint16, (n, NQ, D))
+                assert np.array_equal(got, want), f"replay {rep}"
+                # eager work between replays: the regular call on the default stream
+                ctx.decode_attn(0, seqs, q, o_ref, gate=gate, out_dtype=kvc.DTYPE_BF16)
+                ctx.sync()
+                assert np.array_equal(o_ref.download(np.uint16, (n, NQ, D)), want)
+        finally:
+            h.graph_destroy(graph)
+        for b_ in (q, gate, o_ref, o_st):
+            b_.free()
