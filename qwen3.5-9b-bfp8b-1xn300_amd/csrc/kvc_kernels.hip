@@ -2079,6 +2079,13 @@ __device__ __forceinline__ float dn_silu(float x) {
         return silu_f(x);
 }
 
+// Workgroup barrier for LDS traffic only: this wave's LDS accesses complete,
+// then s_barrier.  Unlike __syncthreads() (a release fence), it does not wait
+// for outstanding global loads, so inputs requested ahead of their use stay in
+// flight across it.  Only for kernels whose waves exchange data through LDS
+// alone.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // sum over the 16 lanes of a DPP row (every lane gets the sum)
 __device__ __forceinline__ float sum16(float x) {
     x += dpp<kDppXor1>(x);
@@ -2194,7 +2201,7 @@ __device__ __forceinline__ void nt_st4(float* p, float x, float y, float z, floa
     __builtin_nontemporal_store(f32x4{x, y, z, w}, reinterpret_cast<f32x4*>(p));
 }
 
-template <bool BF16IN, bool REF>
+template <bool BF16IN, bool REF, bool MULTI>
 __global__ __launch_bounds__(kDnThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void deltanet_kernel(DeltaNetArgs a) {
 #pragma clang fp contract(off)
@@ -2205,14 +2212,25 @@ void deltanet_kernel(DeltaNetArgs a) {
     //      place (dn_qk, same lanes as the one-token kernel); lanes 0..2nb-1
     //      compute (decay, beta) of (token, v-head);
     //   P3 (sequential) every lane updates its 8 state rows token after token
-    //      (dn_row) with no barrier inside the block -> os[tok][vl][row];
+    //      (dn_row) with no barrier inside the block -> os[tok][vl][row], in
+    //      two halves of 4 rows: each row's recurrence is independent of the
+    //      others, so the first half runs while the second half's state is
+    //      still arriving, and in the last block the first half's state is
+    //      stored while the second half runs;
     //   P4 (token-parallel) wave w writes the gated RMSNorm of (token,
     //      v-head) pairs w, w + 8, ...
-    // Three barriers per block instead of two per token; the arithmetic is
-    // that of the one-token kernel, so a token gives the same bits.
+    // A block's inputs (conv inputs and taps, gate inputs and weights, z) are
+    // requested before the state (first block) or during the block before,
+    // and are used or staged in LDS in P1, so no phase waits for state loads
+    // it does not read and no input stays live in registers through the
+    // delta rule.  The barriers wait for LDS traffic only.  The
+    // arithmetic is that of the one-token kernel, so a token gives the same
+    // bits.
     __shared__ float xs[kDnBlk][4 * 128];        // q_kh, k_kh, v_vh0, v_vh1 of each token
     __shared__ float2 gs[kDnBlk][2];             // (decay, beta) per token and v-head
     __shared__ float os[kDnBlk][2][kSsmDv];      // scaled recurrence outputs
+    __shared__ float zs[2][kDnBlk][2][kSsmDv];   // z of each token and v-head (by block parity)
+    __shared__ float nws[kSsmDv];                // output-norm weights
     const int b = blockIdx.x;
     const int s = b / kSsmKHeads;
     const int kh = b - s * kSsmKHeads;
@@ -2227,6 +2245,44 @@ void deltanet_kernel(DeltaNetArgs a) {
     uint8_t* slot = a.state + (size_t)a.slot[s] * a.state_bytes + a.layer_off;
     float* S = reinterpret_cast<float*>(slot) + (size_t)vh * kSsmDv * kSsmDk + col0;
     float* conv = reinterpret_cast<float*>(slot + a.rec_bytes);
+    constexpr size_t kZ = kSsmC, kAlpha = kSsmC + kSsmVHeads * kSsmDv, kBeta = kAlpha + kSsmVHeads;
+    constexpr int kZPer = kDnBlk * 2 * kSsmDv / kDnThreads;  // z values each thread stages
+    const size_t prow0 = (size_t)s * a.n_tok * kSsmProj;
+    const int g16 = t >> 4;  // 16-lane group of P2
+    const int ch = dn_channel(t, kh);
+    // gate thread t < 2 kDnBlk serves (token t / 2, v-head t % 2)
+    const int gt = t >> 1, gvh = kh + kSsmKHeads * (t & 1);
+
+    // one block's inputs: conv inputs and taps of channel ch, the gate
+    // inputs and weights, and kZPer z values (flat index t + 512 j of
+    // [token][v-head][dim])
+    float xin[kDnBlk], zr[kZPer];
+    float4 cw;
+    float gal = 0.f, gbr = 0.f, gdtb = 0.f, gav = 0.f;
+    auto load_inputs = [&](int tok0) {
+        cw = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch], a.conv_w[3 * kSsmC + ch]);
+#pragma unroll
+        for (int i = 0; i < kDnBlk; i++)
+            xin[i] = tok0 + i < a.n_tok ? load_f<BF16IN>(a.proj, prow0 + (size_t)(tok0 + i) * kSsmProj + ch) : 0.f;
+        if (t < 2 * kDnBlk && tok0 + gt < a.n_tok) {
+            const size_t row = prow0 + (size_t)(tok0 + gt) * kSsmProj;
+            gal = load_f<BF16IN>(a.proj, row + kAlpha + gvh);
+            gbr = load_f<BF16IN>(a.proj, row + kBeta + gvh);
+            gdtb = a.dt_bias[gvh];
+            gav = a.a[gvh];
+        }
+#pragma unroll
+        for (int j = 0; j < kZPer; j++) {
+            const int f = t + kDnThreads * j, zt = f / (2 * kSsmDv), zv = (f / kSsmDv) & 1, d = f % kSsmDv;
+            zr[j] = tok0 + zt < a.n_tok
+                        ? load_f<BF16IN>(a.proj, prow0 + (size_t)(tok0 + zt) * kSsmProj + kZ +
+                                                     (size_t)(kh + kSsmKHeads * zv) * kSsmDv + d)
+                        : 0.f;
+        }
+    };
+    float w0 = conv[ch], w1 = conv[kSsmC + ch], w2 = conv[2 * kSsmC + ch];  // window, oldest first
+    const float nwr = t < kSsmDv ? a.norm_w[t] : 0.f;
+    load_inputs(0);
 
     float st[kDnRows][kDnCols];
 #pragma unroll
@@ -2237,23 +2293,24 @@ void deltanet_kernel(DeltaNetArgs a) {
         st[r][0] = x0.x; st[r][1] = x0.y; st[r][2] = x0.z; st[r][3] = x0.w;
         st[r][4] = x1.x; st[r][5] = x1.y; st[r][6] = x1.z; st[r][7] = x1.w;
     }
-    const int ch = dn_channel(t, kh);
-    const float4 cw = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch],
-                                  a.conv_w[3 * kSsmC + ch]);
-    float w0 = conv[ch], w1 = conv[kSsmC + ch], w2 = conv[2 * kSsmC + ch];  // window, oldest first
-    constexpr size_t kZ = kSsmC, kAlpha = kSsmC + kSsmVHeads * kSsmDv, kBeta = kAlpha + kSsmVHeads;
-    const size_t prow0 = (size_t)s * a.n_tok * kSsmProj;
-    const int g16 = t >> 4;  // 16-lane group of P2
+    if (t < kSsmDv) nws[t] = nwr;
 
-    // each block's conv inputs are requested during the previous block
-    float xin[kDnBlk];
+    // one block of nb tokens from tok0; LAST: the call's last block, which
+    // stores the state (each half right after its recurrence).  A second
+    // block requests its inputs at its start (the state has arrived by then).
+    auto run_block = [&](auto last_c, int tok0, int nb) {
+        constexpr bool LAST = decltype(last_c)::value;
+        const int zb = (tok0 / kDnBlk) & 1;
+        if (tok0 > 0) load_inputs(tok0);
+        // P1: conv1d + SiLU, window pushed per token; gates; z staged (the
+        // previous block's P3 is done with gs, and its P4 reads the other zs)
+        if (t < 2 * nb) {
+            float decay, beta;
+            dn_gates<REF>(gal, gbr, gdtb, gav, decay, beta);
+            gs[gt][t & 1] = make_float2(decay, beta);
+        }
 #pragma unroll
-    for (int i = 0; i < kDnBlk; i++)
-        xin[i] = i < a.n_tok ? load_f<BF16IN>(a.proj, prow0 + (size_t)i * kSsmProj + ch) : 0.f;
-
-    for (int tok0 = 0; tok0 < a.n_tok; tok0 += kDnBlk) {
-        const int nb = min(kDnBlk, a.n_tok - tok0);
-        // P1: conv1d + SiLU, window pushed per token
+        for (int j = 0; j < kZPer; j++) (&zs[zb][0][0][0])[t + kDnThreads * j] = zr[j];
 #pragma unroll
         for (int i = 0; i < kDnBlk; i++) {
             if (i < nb) {
@@ -2268,8 +2325,8 @@ void deltanet_kernel(DeltaNetArgs a) {
                 w2 = x;
             }
         }
-        __syncthreads();
-        // P2: q/k normalisation in place, gates
+        lds_barrier();
+        // P2: q/k normalisation in place
         if (g16 < nb) {
             float q[kDnCols], k[kDnCols];
             dn_qk(xs[g16], col0, a.eps, q, k);
@@ -2280,66 +2337,70 @@ void deltanet_kernel(DeltaNetArgs a) {
                 *reinterpret_cast<float4*>(&xs[g16][128 + c]) = make_float4(k[j], k[j + 1], k[j + 2], k[j + 3]);
             }
         }
-        if (t < 2 * nb) {
-            const int gt = t >> 1, gvh = kh + kSsmKHeads * (t & 1);
-            const size_t row = prow0 + (size_t)(tok0 + gt) * kSsmProj;
-            float decay, beta;
-            dn_gates<REF>(load_f<BF16IN>(a.proj, row + kAlpha + gvh), load_f<BF16IN>(a.proj, row + kBeta + gvh),
-                     a.dt_bias[gvh], a.a[gvh], decay, beta);
-            gs[gt][t & 1] = make_float2(decay, beta);
-        }
-        __syncthreads();
-        // P3: the delta rule, token after token; the 16 lanes of a row hold
-        // the same output and all store it (one LDS word, same value)
-        for (int i = 0; i < nb; i++) {
-            float q[kDnCols], k[kDnCols];
+        lds_barrier();
+        // P3: the delta rule, token after token, in two halves of the lane's
+        // rows; the 16 lanes of a row hold the same output and all store it
+        // (one LDS word, same value)
+        auto half = [&](auto hc) {
+            constexpr int r0 = decltype(hc)::value * kDnRows / 2;
+            for (int i = 0; i < nb; i++) {
+                float q[kDnCols], k[kDnCols];
 #pragma unroll
-            for (int j = 0; j < kDnCols; j += 4) {
-                const int c = col0 + (j ? kSsmDk / 2 : 0);
-                const float4 qq = *reinterpret_cast<const float4*>(&xs[i][c]);
-                const float4 kk = *reinterpret_cast<const float4*>(&xs[i][128 + c]);
-                q[j] = qq.x; q[j + 1] = qq.y; q[j + 2] = qq.z; q[j + 3] = qq.w;
-                k[j] = kk.x; k[j + 1] = kk.y; k[j + 2] = kk.z; k[j + 3] = kk.w;
+                for (int j = 0; j < kDnCols; j += 4) {
+                    const int c = col0 + (j ? kSsmDk / 2 : 0);
+                    const float4 qq = *reinterpret_cast<const float4*>(&xs[i][c]);
+                    const float4 kk = *reinterpret_cast<const float4*>(&xs[i][128 + c]);
+                    q[j] = qq.x; q[j + 1] = qq.y; q[j + 2] = qq.z; q[j + 3] = qq.w;
+                    k[j] = kk.x; k[j + 1] = kk.y; k[j + 2] = kk.z; k[j + 3] = kk.w;
+                }
+                const float2 gb = gs[i][vl];
+#pragma unroll
+                for (int r = r0; r < r0 + kDnRows / 2; r++)
+                    os[i][vl][rbase + 4 * r] =
+                        dn_row(st[r], k, q, gb.x, gb.y, xs[i][256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
             }
-            const float2 gb = gs[i][vl];
+            if constexpr (LAST) {
 #pragma unroll
-            for (int r = 0; r < kDnRows; r++)
-                os[i][vl][rbase + 4 * r] =
-                    dn_row(st[r], k, q, gb.x, gb.y, xs[i][256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
-        }
-        __syncthreads();
-        // next block's inputs (requested here, not earlier, so that they do
-        // not hold registers through the delta-rule pass)
-        const int ntok0 = tok0 + kDnBlk;
-#pragma unroll
-        for (int i = 0; i < kDnBlk; i++)
-            if (ntok0 + i < a.n_tok) xin[i] = load_f<BF16IN>(a.proj, prow0 + (size_t)(ntok0 + i) * kSsmProj + ch);
+                for (int r = r0; r < r0 + kDnRows / 2; r++) {
+                    float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
+                    nt_st4(dst, st[r][0], st[r][1], st[r][2], st[r][3]);
+                    nt_st4(dst + kSsmDk / 2, st[r][4], st[r][5], st[r][6], st[r][7]);
+                }
+            }
+        };
+        half(std::integral_constant<int, 0>{});
+        half(std::integral_constant<int, 1>{});
+        lds_barrier();
         // P4: gated RMSNorm of (token, v-head) pairs, all 128 dims per wave
-        for (int p = wave; p < 2 * nb; p += kDnThreads / 64) {
-            const int pt = p >> 1, pvl = p & 1, pvh = kh + kSsmKHeads * pvl;
-            const float* o_row = os[pt][pvl];
+#pragma unroll
+        for (int pi = 0; pi < 2; pi++) {
+            const int p = wave + 8 * pi;
+            if (p >= 2 * nb) break;
+            const int pt = p >> 1, pv = p & 1, pvh = kh + kSsmKHeads * pv;
+            const float* o_row = os[pt][pv];
             const float o0 = o_row[lane], o1 = o_row[lane + 64];
             const float ss = wave_sum(fmaf(o0, o0, o1 * o1));
             const float rms = dn_rsqrt(ss / kSsmDv + a.eps);
-            const size_t row = prow0 + (size_t)(tok0 + pt) * kSsmProj;
             const size_t out_row = ((size_t)s * a.n_tok + tok0 + pt) * (kSsmVHeads * kSsmDv) + (size_t)pvh * kSsmDv;
 #pragma unroll
             for (int h2 = 0; h2 < 2; h2++) {
                 const int d = lane + 64 * h2;
-                const float z = load_f<BF16IN>(a.proj, row + kZ + (size_t)pvh * kSsmDv + d);
-                const float y = o_row[d] * rms * a.norm_w[d] * dn_silu<REF>(z);
+                const float y = o_row[d] * rms * nws[d] * dn_silu<REF>(zs[zb][pt][pv][d]);
                 if (a.out_bf16)
                     static_cast<uint16_t*>(a.out)[out_row + d] = (uint16_t)f32_to_bf16_rne(y);
                 else
                     static_cast<float*>(a.out)[out_row + d] = y;
             }
         }
-    }
-#pragma unroll
-    for (int r = 0; r < kDnRows; r++) {
-        float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
-        nt_st4(dst, st[r][0], st[r][1], st[r][2], st[r][3]);
-        nt_st4(dst + kSsmDk / 2, st[r][4], st[r][5], st[r][6], st[r][7]);
+    };
+    // MULTI: kDnBlk + 1 .. 2 kDnBlk - 1 tokens (longer calls run the matrix
+    // form); otherwise 2 .. kDnBlk.  Separate instantiations keep the common
+    // one-block call free of the second block's register pressure.
+    if constexpr (MULTI) {
+        run_block(std::false_type{}, 0, kDnBlk);
+        run_block(std::true_type{}, kDnBlk, a.n_tok - kDnBlk);
+    } else {
+        run_block(std::true_type{}, 0, a.n_tok);
     }
     conv[ch] = w0;
     conv[kSsmC + ch] = w1;
@@ -2375,13 +2436,6 @@ void deltanet_kernel(DeltaNetArgs a) {
 constexpr int kDnChunk = 16;
 
 __device__ __forceinline__ int dn_sigma(int r) { return 4 * (r & 3) + (r >> 2); }
-
-// Workgroup barrier for LDS traffic only: this wave's LDS accesses complete,
-// then s_barrier.  Unlike __syncthreads() (a release fence), it does not wait
-// for outstanding global loads, so inputs requested ahead of their use stay in
-// flight across it.  Only for kernels whose waves exchange data through LDS
-// alone.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // One wave: A B for 16 x 16 row-major fp32 matrices in LDS; lane (g, c)
 // returns rows 4 g .. 4 g + 3 of column c.
@@ -3295,10 +3349,15 @@ static void launch_deltanet_t(const DeltaNetArgs& a, hipStream_t stream) {
             hipLaunchKernelGGL((deltanet_mfma_kernel<false, true, REF>), mgrid, mblock, 0, stream, a);
         else
             hipLaunchKernelGGL((deltanet_mfma_kernel<false, false, REF>), mgrid, mblock, 0, stream, a);
+    } else if (a.n_tok > kDnBlk) {
+        if (a.in_bf16)
+            hipLaunchKernelGGL((deltanet_kernel<true, REF, true>), grid, block, 0, stream, a);
+        else
+            hipLaunchKernelGGL((deltanet_kernel<false, REF, true>), grid, block, 0, stream, a);
     } else if (a.in_bf16) {
-        hipLaunchKernelGGL((deltanet_kernel<true, REF>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((deltanet_kernel<true, REF, false>), grid, block, 0, stream, a);
     } else {
-        hipLaunchKernelGGL((deltanet_kernel<false, REF>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((deltanet_kernel<false, REF, false>), grid, block, 0, stream, a);
     }
 }
 
