@@ -2212,11 +2212,8 @@ void deltanet_kernel(DeltaNetArgs a) {
     //      place (dn_qk, same lanes as the one-token kernel); lanes 0..2nb-1
     //      compute (decay, beta) of (token, v-head);
     //   P3 (sequential) every lane updates its 8 state rows token after token
-    //      (dn_row) with no barrier inside the block -> os[tok][vl][row], in
-    //      two halves of 4 rows: each row's recurrence is independent of the
-    //      others, so the first half runs while the second half's state is
-    //      still arriving, and in the last block the first half's state is
-    //      stored while the second half runs;
+    //      (dn_row) with no barrier inside the block -> os[tok][vl][row]; the
+    //      last block stores the state right after it;
     //   P4 (token-parallel) wave w writes the gated RMSNorm of (token,
     //      v-head) pairs w, w + 8, ...
     // A block's inputs (conv inputs and taps, gate inputs and weights, z) are
@@ -2255,17 +2252,19 @@ void deltanet_kernel(DeltaNetArgs a) {
 
     // one block's inputs: conv inputs and taps of channel ch, the gate
     // inputs and weights, and kZPer z values (flat index t + 512 j of
-    // [token][v-head][dim])
+    // [token][v-head][dim]).  Every load is unconditional, its token index
+    // clamped to the call (values of tokens past the end are never used): a
+    // load under a branch is followed by a wait for it at the branch's end.
     float xin[kDnBlk], zr[kZPer];
     float4 cw;
-    float gal = 0.f, gbr = 0.f, gdtb = 0.f, gav = 0.f;
+    float gal, gbr, gdtb, gav;
+    auto tok_row = [&](int tok) { return prow0 + (size_t)min(tok, a.n_tok - 1) * kSsmProj; };
     auto load_inputs = [&](int tok0) {
         cw = make_float4(a.conv_w[ch], a.conv_w[kSsmC + ch], a.conv_w[2 * kSsmC + ch], a.conv_w[3 * kSsmC + ch]);
 #pragma unroll
-        for (int i = 0; i < kDnBlk; i++)
-            xin[i] = tok0 + i < a.n_tok ? load_f<BF16IN>(a.proj, prow0 + (size_t)(tok0 + i) * kSsmProj + ch) : 0.f;
-        if (t < 2 * kDnBlk && tok0 + gt < a.n_tok) {
-            const size_t row = prow0 + (size_t)(tok0 + gt) * kSsmProj;
+        for (int i = 0; i < kDnBlk; i++) xin[i] = load_f<BF16IN>(a.proj, tok_row(tok0 + i) + ch);
+        {
+            const size_t row = tok_row(tok0 + (gt & (kDnBlk - 1)));
             gal = load_f<BF16IN>(a.proj, row + kAlpha + gvh);
             gbr = load_f<BF16IN>(a.proj, row + kBeta + gvh);
             gdtb = a.dt_bias[gvh];
@@ -2274,14 +2273,11 @@ void deltanet_kernel(DeltaNetArgs a) {
 #pragma unroll
         for (int j = 0; j < kZPer; j++) {
             const int f = t + kDnThreads * j, zt = f / (2 * kSsmDv), zv = (f / kSsmDv) & 1, d = f % kSsmDv;
-            zr[j] = tok0 + zt < a.n_tok
-                        ? load_f<BF16IN>(a.proj, prow0 + (size_t)(tok0 + zt) * kSsmProj + kZ +
-                                                     (size_t)(kh + kSsmKHeads * zv) * kSsmDv + d)
-                        : 0.f;
+            zr[j] = load_f<BF16IN>(a.proj, tok_row(tok0 + zt) + kZ + (size_t)(kh + kSsmKHeads * zv) * kSsmDv + d);
         }
     };
     float w0 = conv[ch], w1 = conv[kSsmC + ch], w2 = conv[2 * kSsmC + ch];  // window, oldest first
-    const float nwr = t < kSsmDv ? a.norm_w[t] : 0.f;
+    const float nwr = a.norm_w[t & (kSsmDv - 1)];
     load_inputs(0);
 
     float st[kDnRows][kDnCols];
@@ -2293,11 +2289,11 @@ void deltanet_kernel(DeltaNetArgs a) {
         st[r][0] = x0.x; st[r][1] = x0.y; st[r][2] = x0.z; st[r][3] = x0.w;
         st[r][4] = x1.x; st[r][5] = x1.y; st[r][6] = x1.z; st[r][7] = x1.w;
     }
-    if (t < kSsmDv) nws[t] = nwr;
+    nws[t & (kSsmDv - 1)] = nwr;  // every thread: no branch for the load to sink into
 
     // one block of nb tokens from tok0; LAST: the call's last block, which
-    // stores the state (each half right after its recurrence).  A second
-    // block requests its inputs at its start (the state has arrived by then).
+    // stores the state.  A second block requests its inputs at its start
+    // (the state has arrived by then).
     auto run_block = [&](auto last_c, int tok0, int nb) {
         constexpr bool LAST = decltype(last_c)::value;
         const int zb = (tok0 / kDnBlk) & 1;
@@ -2338,11 +2334,9 @@ void deltanet_kernel(DeltaNetArgs a) {
             }
         }
         lds_barrier();
-        // P3: the delta rule, token after token, in two halves of the lane's
-        // rows; the 16 lanes of a row hold the same output and all store it
-        // (one LDS word, same value)
-        auto half = [&](auto hc) {
-            constexpr int r0 = decltype(hc)::value * kDnRows / 2;
+        // P3: the delta rule, token after token; the 16 lanes of a row hold
+        // the same output and all store it (one LDS word, same value)
+        {
             for (int i = 0; i < nb; i++) {
                 float q[kDnCols], k[kDnCols];
 #pragma unroll
@@ -2355,21 +2349,19 @@ void deltanet_kernel(DeltaNetArgs a) {
                 }
                 const float2 gb = gs[i][vl];
 #pragma unroll
-                for (int r = r0; r < r0 + kDnRows / 2; r++)
+                for (int r = 0; r < kDnRows; r++)
                     os[i][vl][rbase + 4 * r] =
                         dn_row(st[r], k, q, gb.x, gb.y, xs[i][256 + vl * 128 + rbase + 4 * r]) * a.out_scale;
             }
             if constexpr (LAST) {
 #pragma unroll
-                for (int r = r0; r < r0 + kDnRows / 2; r++) {
+                for (int r = 0; r < kDnRows; r++) {
                     float* dst = S + (size_t)(rbase + 4 * r) * kSsmDk;
                     nt_st4(dst, st[r][0], st[r][1], st[r][2], st[r][3]);
                     nt_st4(dst + kSsmDk / 2, st[r][4], st[r][5], st[r][6], st[r][7]);
                 }
             }
-        };
-        half(std::integral_constant<int, 0>{});
-        half(std::integral_constant<int, 1>{});
+        }
         lds_barrier();
         // P4: gated RMSNorm of (token, v-head) pairs, all 128 dims per wave
 #pragma unroll
