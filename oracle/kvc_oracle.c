@@ -179,6 +179,11 @@ float orc_fast_expf_rne(float x) {
     return f;
 }
 
+/* mode 1 is fast_sigmoidf's source expression with an IEEE division
+ * (:2358-2360).  The reference's fast-math build may compile the division as
+ * an approximate reciprocal and a Newton step: over every finite bf16 input
+ * its Zen 4 build differs from this model by at most 1 ulp (subnormal
+ * quotients aside), as tests/test_fastmath_forms.py measures. */
 float orc_sigmoid(float x, int mode) {
     if (mode == 1) return 1.0f / (1.0f + orc_fast_expf(-x)); /* :2358-2360 */
     return 1.0f / (1.0f + expf(-x));
