@@ -2417,9 +2417,11 @@ void deltanet_kernel(DeltaNetArgs a) {
 //
 // Wave w holds v-columns 32 (w % 4) .. +31 of v-head kh + 16 (w / 4): its
 // state slice is kept as MFMA B fragments, lane (g = l / 16, c = l % 16)
-// holding S^T[32 g + s][i0 + c] for s = 0..31 (the k-dim order of every
-// product is k = 32 g + s), so the state update's MFMA result lands in that
-// same layout when its A rows are taken in the order 32 (r / 4) + 4 m + r % 4.
+// holding S^T[16 m + 4 g + e][i0 + c] in register e of fragment m (the k-dim
+// order of every product is k = 16 m + 4 g + e, so the four lane groups of a
+// state row hold 64 contiguous bytes of it per fragment), and the state
+// update's MFMA m, whose A rows are k = 16 m .. 16 m + 15, lands in that same
+// layout.
 // Token rows of W1, U and O are taken in the order sigma(r) = 4 (r % 4) + r / 4
 // so that lane group g, register r of each of them is token 4 r + g: the
 // B fragment of a 4-token step j of the next product is then register j.
@@ -2505,7 +2507,10 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
     // other's registers.
     if (wave < kDnMathWaves) {
         // v-head hl, v-columns ibase .. +31 (two 16-column tiles); state
-        // slice as B fragments: st[vt][m] = S^T[32 g + 4 m .. +3][ibase + 16 vt + c]
+        // slice as B fragments: st[vt][m] = S^T[16 m + 4 g .. +3][ibase + 16 vt + c].
+        // The k order k = 16 m + 4 g + e (every product uses it) puts the four
+        // lane groups of a state row on 64 contiguous bytes, so each load or
+        // store instruction of a slice covers 16 rows x 64 B
         const int hl = wave >> 2;
         const int ibase = 32 * (wave & 3);
         auto slice_of = [&](int item) {
@@ -2515,17 +2520,17 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
         auto load_state = [&](const float* S) {
 #pragma unroll
             for (int vt = 0; vt < 2; vt++) {
-                const float* src = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
+                const float* src = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 4 * g;
 #pragma unroll
-                for (int m = 0; m < 8; m++) st[vt][m] = *reinterpret_cast<const f32x4*>(src + 4 * m);
+                for (int m = 0; m < 8; m++) st[vt][m] = *reinterpret_cast<const f32x4*>(src + 16 * m);
             }
         };
         auto store_state = [&](float* S) {
 #pragma unroll
             for (int vt = 0; vt < 2; vt++) {
-                float* dst = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 32 * g;
+                float* dst = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 4 * g;
 #pragma unroll
-                for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 4 * m) = st[vt][m];
+                for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 16 * m) = st[vt][m];
             }
         };
         load_state(slice_of(item_at(0)));
@@ -2543,12 +2548,12 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             // Phase A: W1 = K S^T and W2 = Q S^T (rows in sigma order)
             f32x4 w1a[2] = {}, w2a[2] = {};
             {
-                const float* kr = &x[dn_sigma(c)][128 + 32 * g];
-                const float* qr = &x[dn_sigma(c)][32 * g];
+                const float* kr = &x[dn_sigma(c)][128 + 4 * g];
+                const float* qr = &x[dn_sigma(c)][4 * g];
 #pragma unroll
                 for (int m = 0; m < 8; m++) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 4 * m);
-                    const float4 q4 = *reinterpret_cast<const float4*>(qr + 4 * m);
+                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 16 * m);
+                    const float4 q4 = *reinterpret_cast<const float4*>(qr + 16 * m);
                     const float ka[4] = {k4.x, k4.y, k4.z, k4.w}, qa[4] = {q4.x, q4.y, q4.z, q4.w};
 #pragma unroll
                     for (int e = 0; e < 4; e++)
@@ -2597,7 +2602,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 const float f = fc[cur][hl][tok];
 #pragma unroll
                 for (int m = 0; m < 8; m++) {
-                    const float ak = f * x[tok][128 + 32 * (c >> 2) + 4 * m + (c & 3)];
+                    const float ak = f * x[tok][128 + 16 * m + c];
 #pragma unroll
                     for (int vt = 0; vt < 2; vt++)
                         st[vt][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak, uu[vt][j], st[vt][m], 0, 0, 0);
