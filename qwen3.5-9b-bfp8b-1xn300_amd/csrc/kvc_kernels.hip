@@ -2385,7 +2385,7 @@ void deltanet_kernel(DeltaNetArgs a) {
             }
         }
     };
-    // MULTI: kDnBlk + 1 .. 2 kDnBlk - 1 tokens (longer calls run the matrix
+    // MULTI: kDnBlk + 1 .. kDnMatrixMin - 1 tokens (longer calls run the matrix
     // form); otherwise 2 .. kDnBlk.  Separate instantiations keep the common
     // one-block call free of the second block's register pressure.
     if constexpr (MULTI) {
@@ -2428,6 +2428,12 @@ void deltanet_kernel(DeltaNetArgs a) {
 // Tokens past the end of the last chunk enter as zero rows with beta = 0
 // and log decay 0, which leaves U, O and S unchanged.
 constexpr int kDnChunk = 16;
+// Calls of this many tokens or more run the matrix form (one partial block
+// below 16).  Measured at config e (64 sessions): the blocked kernel takes
+// 84 / 97 us per layer at 12 / 15 tokens, the matrix form 91.5 / 92.2; the two
+// meet at 14.
+constexpr int kDnMatrixMin = 14;
+static_assert(kDnMatrixMin <= 2 * kDnBlk, "the blocked kernel covers calls of at most two blocks");
 
 __device__ __forceinline__ int dn_sigma(int r) { return 4 * (r & 3) + (r >> 2); }
 
@@ -3324,7 +3330,7 @@ static void launch_deltanet_t(const DeltaNetArgs& a, hipStream_t stream) {
             hipLaunchKernelGGL((deltanet_decode_kernel<true, REF>), grid, block, 0, stream, a);
         else
             hipLaunchKernelGGL((deltanet_decode_kernel<false, REF>), grid, block, 0, stream, a);
-    } else if (a.n_tok >= kDnChunk) {
+    } else if (a.n_tok >= kDnMatrixMin) {
         // persistent: at most one workgroup per CU (its LDS needs a CU); the
         // CU count of the current device is looked up once per process
         static std::atomic<int> cu_count{0};

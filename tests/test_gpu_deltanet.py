@@ -134,6 +134,15 @@ def test_deltanet_chunk_and_bf16_out():
     run_case(kvc.DTYPE_BF16, kvc.DTYPE_BF16, n_tok=3, n_seqs=1, seed=7300)
 
 
+@pytest.mark.parametrize("n_tok,in_dtype", [(8, kvc.DTYPE_BF16), (9, kvc.DTYPE_F32), (13, kvc.DTYPE_BF16)])
+def test_deltanet_blocked_one_and_two_blocks(n_tok, in_dtype):
+    """The blocked kernel's two instantiations: one full block of 8 tokens,
+    and two blocks (9 and 13 tokens, the second block's inputs requested at
+    its start)."""
+    say(f"deltanet blocked kernel, {n_tok} tokens")
+    run_case(in_dtype, kvc.DTYPE_F32, n_tok=n_tok, n_seqs=3, seed=7400 + n_tok)
+
+
 def test_deltanet_resume_from_snapshot_is_bit_identical():
     """Decode resumed from a restored snapshot equals the same decode run
     straight from the saved state, bit for bit (the whole resume runs on the
@@ -256,10 +265,11 @@ def test_deltanet_state_is_zero_after_create_and_reset():
         b_.free()
 
 
-@pytest.mark.parametrize("n_tok", [16, 37, 128])
+@pytest.mark.parametrize("n_tok", [14, 16, 37, 128])
 def test_deltanet_matrix_form_chunks_match_oracle(n_tok):
-    """Calls of 16 or more tokens take the matrix (WY) form over 16-token
-    blocks on fp32 MFMA; 37 tokens end in a partial block.  Every token's
+    """Calls of 14 or more tokens take the matrix (WY) form over 16-token
+    blocks on fp32 MFMA; 14 tokens are one partial block and 37 tokens end
+    in one.  Every token's
     output and the final state are held to the same fp32 bar as the
     token-by-token kernels."""
     say(f"deltanet matrix form, {n_tok} tokens")
