@@ -3,7 +3,8 @@ the tests and bench need for device buffers, streams and events.
 
 The product is the C ABI; this module is the thin FFI stub a caller in Python
 would write.  It loads the in-tree libkvc.so and raises if it is missing --
-there is no fallback path.  HIP is reached through the same libamdhip64 the
+there is no fallback path.  KVC_LIB_PATH, when set, names another build of
+the same library instead (the tests use it for a host-sanitizer build).  HIP is reached through the same libamdhip64 the
 library links (loaded after libkvc.so, so the process holds one runtime);
 torch is not imported.
 """
@@ -16,7 +17,7 @@ from pathlib import Path
 import numpy as np
 
 PKG_DIR = Path(__file__).resolve().parent
-LIB_PATH = PKG_DIR / "libkvc.so"
+LIB_PATH = Path(os.environ["KVC_LIB_PATH"]) if os.environ.get("KVC_LIB_PATH") else PKG_DIR / "libkvc.so"
 
 KVC_OK = 0
 KVC_ERR_INVALID = -1
