@@ -9,7 +9,8 @@ chunk lengths that are not multiples of the 32-row query block.  A decode
 loop then appends one token per step across several block boundaries and
 checks every step.  Tolerances are the north-star ones (max |diff| <= 2e-2,
 relative RMS <= 1e-2) plus the tighter relative-RMS bound the other parity
-tests use.
+tests use.  The Gated-DeltaNet cases at the end cross token count, input and
+output dtype and math mode, at the DeltaNet tests' fp32 bar.
 """
 import numpy as np
 import pytest
@@ -194,3 +195,28 @@ def test_decode_loop_across_blocks(chunk):
         for i, s in enumerate(seqs):
             mk, mv = m.get(s, 0)
             assert np.array_equal(got[i][0], mk) and np.array_equal(got[i][1], mv), s
+
+
+# Gated-DeltaNet step: token counts across the blocked kernel (2..13, one and
+# two blocks) and the matrix form (14 and more, partial last blocks), with
+# every pairing of input and output dtype and both math modes; the state, the
+# conv window and every token's output are checked against the oracle
+# (run_case of test_gpu_deltanet).
+DN_CASES = [
+    (2, kvc.DTYPE_F32, kvc.DTYPE_BF16, 5, False),
+    (6, kvc.DTYPE_BF16, kvc.DTYPE_BF16, 4, True),
+    (11, kvc.DTYPE_F32, kvc.DTYPE_F32, 3, False),
+    (12, kvc.DTYPE_BF16, kvc.DTYPE_BF16, 6, False),
+    (15, kvc.DTYPE_F32, kvc.DTYPE_BF16, 2, True),
+    (17, kvc.DTYPE_BF16, kvc.DTYPE_F32, 3, False),
+    (31, kvc.DTYPE_F32, kvc.DTYPE_F32, 2, False),
+    (48, kvc.DTYPE_BF16, kvc.DTYPE_BF16, 5, True),
+]
+
+
+@pytest.mark.parametrize("n_tok,in_dtype,out_dtype,n_seqs,exact", DN_CASES)
+def test_deltanet_sweep(n_tok, in_dtype, out_dtype, n_seqs, exact):
+    from test_gpu_deltanet import run_case
+
+    say(f"deltanet sweep: {n_tok} tokens, {n_seqs} sessions, in {in_dtype} out {out_dtype} exact={exact}")
+    run_case(in_dtype, out_dtype, n_tok=n_tok, n_seqs=n_seqs, seed=11000 + 7 * n_tok, exact=exact)
