@@ -744,7 +744,8 @@ int kvc_seq_create(kvc_ctx* c, int32_t* seq) {
 }
 
 int kvc_seq_reset(kvc_ctx* c, int32_t seq) {
-    if (!c || !seq_ok(c, seq)) return set_err(KVC_ERR_INVALID, "sequence %d is not live", seq);
+    if (!c) return set_err(KVC_ERR_INVALID, "null context");
+    if (!seq_ok(c, seq)) return set_err(KVC_ERR_INVALID, "sequence %d is not live", seq);
     release_tail(c, seq, 0);
     Seq& s = c->seqs[seq];
     s.len = s.pending = 0;
@@ -764,13 +765,15 @@ int kvc_seq_release(kvc_ctx* c, int32_t seq) {
 }
 
 int kvc_seq_len(kvc_ctx* c, int32_t seq, int32_t* len) {
-    if (!c || !len || !seq_ok(c, seq)) return set_err(KVC_ERR_INVALID, "sequence %d is not live", seq);
+    if (!c || !len) return set_err(KVC_ERR_INVALID, "null argument");
+    if (!seq_ok(c, seq)) return set_err(KVC_ERR_INVALID, "sequence %d is not live", seq);
     *len = c->seqs[seq].len;
     return KVC_OK;
 }
 
 int kvc_seq_truncate(kvc_ctx* c, int32_t seq, int32_t len) {
-    if (!c || !seq_ok(c, seq)) return set_err(KVC_ERR_INVALID, "sequence %d is not live", seq);
+    if (!c) return set_err(KVC_ERR_INVALID, "null context");
+    if (!seq_ok(c, seq)) return set_err(KVC_ERR_INVALID, "sequence %d is not live", seq);
     Seq& s = c->seqs[seq];
     if (s.pending) return set_err(KVC_ERR_STATE, "sequence %d has %d uncommitted tokens", seq, s.pending);
     if (len < 0 || len > s.len) return set_err(KVC_ERR_RANGE, "truncate to %d outside [0, %d]", len, s.len);

@@ -349,3 +349,90 @@ def test_hybrid_truncate_stops_keying_by_tokens():
         c.commit([a], 156, T[100:256])
         b = c.seq_create()
         assert c.prefix_match(b, np.concatenate([T[:256], [1]]).astype(np.int32)) == 256
+
+
+def _zero_args(argtypes):
+    """Null pointers and zero scalars for a ctypes argument list."""
+    out = []
+    for t in argtypes:
+        if t in (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64):
+            out.append(0)
+        elif t is ctypes.c_float:
+            out.append(0.0)
+        else:
+            out.append(None)
+    return out
+
+
+def test_null_context_rejected_by_every_entry_point():
+    """Every entry point that takes a context returns KVC_ERR_INVALID for a
+    null one (with every other argument null or zero), and sets the error
+    text; kvc_destroy(NULL) is a no-op, like free(NULL)."""
+    L = kvc.lib()
+    checked = 0
+    for name in kvc.EXPORTS:
+        fn = getattr(L, name)
+        if not fn.argtypes or fn.argtypes[0] is not ctypes.c_void_p:
+            continue
+        rc = fn(*_zero_args(fn.argtypes))
+        if name == "kvc_destroy":
+            assert rc == kvc.KVC_OK
+            continue
+        assert rc == kvc.KVC_ERR_INVALID, (name, rc)
+        assert L.kvc_last_error(), name
+        checked += 1
+    assert checked == len(kvc.EXPORTS) - 5  # all but config_default, create, last_error, abi_version, destroy
+    # kvc_create with a null config or a null output
+    cfg = kvc.Config()
+    L.kvc_config_default(ctypes.byref(cfg))
+    out = ctypes.c_void_p()
+    assert L.kvc_create(None, ctypes.byref(out)) == kvc.KVC_ERR_INVALID
+    assert L.kvc_create(ctypes.byref(cfg), None) == kvc.KVC_ERR_INVALID
+
+
+def test_bad_arguments_rejected_by_host_calls():
+    """The host-side calls reject bad sequence lists, ids, counts and
+    pointers with an error code and leave the bookkeeping unchanged."""
+    L = kvc.lib()
+    with host_ctx() as c:
+        s = c.seq_create()
+        before = (c.stats().free_blocks, c.seq_len(s))
+        n1 = ctypes.c_int32(0)
+        arr = (ctypes.c_int32 * 2)(s, s)
+        bad_id = (ctypes.c_int32 * 1)(99)
+        neg_id = (ctypes.c_int32 * 1)(-1)
+        one = (ctypes.c_int32 * 1)(s)
+        cases = [
+            ("reserve null list", L.kvc_seq_reserve(c.ptr, None, 1, 4, None), kvc.KVC_ERR_INVALID),
+            ("reserve zero seqs", L.kvc_seq_reserve(c.ptr, one, 0, 4, None), kvc.KVC_ERR_INVALID),
+            ("reserve negative seqs", L.kvc_seq_reserve(c.ptr, one, -3, 4, None), kvc.KVC_ERR_INVALID),
+            ("reserve duplicate", L.kvc_seq_reserve(c.ptr, arr, 2, 4, None), kvc.KVC_ERR_INVALID),
+            ("reserve unknown id", L.kvc_seq_reserve(c.ptr, bad_id, 1, 4, None), kvc.KVC_ERR_INVALID),
+            ("reserve negative id", L.kvc_seq_reserve(c.ptr, neg_id, 1, 4, None), kvc.KVC_ERR_INVALID),
+            ("reserve zero tokens", L.kvc_seq_reserve(c.ptr, one, 1, 0, None), kvc.KVC_ERR_INVALID),
+            ("reserve negative tokens", L.kvc_seq_reserve(c.ptr, one, 1, -5, None), kvc.KVC_ERR_INVALID),
+            ("reserve past max_seq_len", L.kvc_seq_reserve(c.ptr, one, 1, 4097, None), kvc.KVC_ERR_RANGE),
+            ("commit nothing reserved", L.kvc_seq_commit(c.ptr, one, 1, 4, None, None), kvc.KVC_ERR_STATE),
+            ("commit unknown id", L.kvc_seq_commit(c.ptr, bad_id, 1, 4, None, None), kvc.KVC_ERR_INVALID),
+            ("len null out", L.kvc_seq_len(c.ptr, s, None), kvc.KVC_ERR_INVALID),
+            ("len unknown id", L.kvc_seq_len(c.ptr, 99, ctypes.byref(n1)), kvc.KVC_ERR_INVALID),
+            ("truncate past end", L.kvc_seq_truncate(c.ptr, s, 1), kvc.KVC_ERR_RANGE),
+            ("truncate negative", L.kvc_seq_truncate(c.ptr, s, -1), kvc.KVC_ERR_RANGE),
+            ("reset unknown id", L.kvc_seq_reset(c.ptr, -7), kvc.KVC_ERR_INVALID),
+            ("release unknown id", L.kvc_seq_release(c.ptr, 12345), kvc.KVC_ERR_INVALID),
+            ("match null out", L.kvc_prefix_match(c.ptr, s, None, 0, None, None), kvc.KVC_ERR_INVALID),
+            ("match null tokens", L.kvc_prefix_match(c.ptr, s, None, 5, ctypes.byref(n1), None),
+             kvc.KVC_ERR_INVALID),
+            ("match negative count", L.kvc_prefix_match(c.ptr, s, None, -1, ctypes.byref(n1), None),
+             kvc.KVC_ERR_INVALID),
+            ("match past max_seq_len", L.kvc_prefix_match(c.ptr, s, (ctypes.c_int32 * 4097)(), 4097,
+                                                          ctypes.byref(n1), None), kvc.KVC_ERR_RANGE),
+            ("snapshot release unknown", L.kvc_snapshot_release(c.ptr, 3), kvc.KVC_ERR_INVALID),
+        ]
+        for what, rc, want in cases:
+            assert rc == want, (what, rc, L.kvc_last_error())
+        assert (c.stats().free_blocks, c.seq_len(s)) == before
+        # and the context still works
+        c.reserve([s], 40)
+        c.commit([s], 40)
+        assert c.seq_len(s) == 40
