@@ -37,7 +37,10 @@
  * Conventions (mirroring the reference's error style, src/engine.cpp:4040-4043):
  *   - every call returns int: KVC_OK (0) or a negative KVC_ERR_*; the message
  *     of the last error on the calling thread is kvc_last_error().  No C++
- *     exception crosses this ABI.
+ *     exception crosses this ABI.  A null context is KVC_ERR_INVALID for every
+ *     call but kvc_destroy, for which it is a no-op (KVC_OK), like free(NULL).
+ *     A rejected device call launches nothing: every argument is checked
+ *     before the first launch.
  *   - a context is single-threaded (the reference serialises generate() with a
  *     mutex, src/server.cpp:20).  Device work of one context must be ordered on
  *     one stream: the split-K workspace and its arrival counters are shared.
