@@ -1138,22 +1138,19 @@ __global__ __launch_bounds__(kWaves * 64) void decode_kernel(DecodeArgs a) {
             Lc = fmaf(Lc, cs, wave_sum(w_l * __uint_as_float(ml[1])));
 #pragma unroll
             for (int j = 0; j < 4; j++) Ac[j] *= cs;
-            // both halves' weights are read for every lane and selected per
-            // lane: a readlane under a lane-dependent condition is compiled
-            // as a divergent branch per partial (measured: 0.7 us per launch
-            // at config b)
-            float we[kNB], wo[kNB];
+            // each lane fetches the weights of its own partials (chunk
+            // k NP + psub lives in lane k NP + psub) with ds_bpermute: no
+            // per-partial readlane or select (a readlane under a
+            // lane-dependent condition compiles to a divergent branch per
+            // partial, measured 0.7 us per launch at config b)
+            float wk[kNB];
 #pragma unroll
-            for (int k = 0; k < kNB; k++) {
-                we[k] = readlane(w_l, k * NP);
-                wo[k] = readlane(w_l, k * NP + 1);
-            }
+            for (int k = 0; k < kNB; k++)
+                wk[k] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (k * NP + psub), __float_as_int(w_l)));
 #pragma unroll
-            for (int k = 0; k < kNB; k++) {
-                const float w = psub ? wo[k] : we[k];
+            for (int k = 0; k < kNB; k++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) Ac[j] = fmaf(w, __uint_as_float(pa[k][j]), Ac[j]);
-            }
+                for (int j = 0; j < 4; j++) Ac[j] = fmaf(wk[k], __uint_as_float(pa[k][j]), Ac[j]);
         }
 #pragma unroll
         for (int j = 0; j < 4; j++) Ac[j] = sum_xor32(Ac[j]);
