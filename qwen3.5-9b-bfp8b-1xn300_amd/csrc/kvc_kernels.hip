@@ -2434,6 +2434,41 @@ static_assert(kDnMatrixMin <= 2 * kDnBlk, "the blocked kernel covers calls of at
 
 __device__ __forceinline__ int dn_sigma(int r) { return 4 * (r & 3) + (r >> 2); }
 
+// Two fp32 values times a power of two s, each as two fp16 parts: h = RNE
+// fp16 of x s (v_fma_mixlo/hi_f16), m = x s - h (exact, v_fma_mix_f32)
+// rounded toward zero to fp16.  x s = h + m within 2^-21 |x s| as long as
+// |x s| < 65504 and m is not subnormal; products on fp16 MFMA then take
+// h.h' + h.m' + m.h' (the dropped m.m' is below 2^-22 of the product).
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ void dn_split2(float x0, float x1, float s, uint32_t& hp, uint32_t& mp) {
+    uint32_t h;
+    float r0, r1;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]" : "=v"(h) : "v"(x0), "v"(s));
+    asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(x1), "v"(s));
+    asm("v_fma_mix_f32 %0, %1, %2, -%3 op_sel_hi:[0,0,1]" : "=v"(r0) : "v"(x0), "v"(s), "v"(h));
+    asm("v_fma_mix_f32 %0, %1, %2, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r1) : "v"(x1), "v"(s), "v"(h));
+    hp = h;
+    mp = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+}
+__device__ __forceinline__ void dn_split8(const float (&x)[8], float s, f16x8_t& h, f16x8_t& m) {
+    u32x4 hw, mw;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t a, b;
+        dn_split2(x[2 * i], x[2 * i + 1], s, a, b);
+        hw[i] = a;
+        mw[i] = b;
+    }
+    h = __builtin_bit_cast(f16x8_t, hw);
+    m = __builtin_bit_cast(f16x8_t, mw);
+}
+__device__ __forceinline__ f32x4 dn_mfma3(const f16x8_t& ah, const f16x8_t& am, const f16x8_t& bh,
+                                          const f16x8_t& bm, f32x4 acc) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bm, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc, 0, 0, 0);
+}
+
 // One wave: A B for 16 x 16 row-major fp32 matrices in LDS; lane (g, c)
 // returns rows 4 g .. 4 g + 3 of column c.
 __device__ __forceinline__ f32x4 dn_m16(const float (*A)[kDnChunk], const float (*B)[kDnChunk], int g, int c) {
@@ -2485,7 +2520,11 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
     __shared__ float qk[kDnChunk][kDnChunk];      // Q K^T
     __shared__ float lm[2][kDnChunk][kDnChunk];   // strict lower of L, then T = L^-1
     __shared__ float mm[2][kDnChunk][kDnChunk];   // e^{g_t - g_s} Q K^T, s <= t
-    __shared__ float sc[2][4][kDnChunk][kDnChunk];  // N^2, N^4, N^8 and the running product
+    __shared__ float sc[2][3][kDnChunk][kDnChunk];  // N^2 (then the running product), N^4, N^8
+    // K and Q of the next block as fp16 MFMA fragments, split into two parts
+    // after a scale of 2^14: [K, Q][32-k step][lane group][h, m][row in
+    // sigma order], 16 B each (consecutive rows on consecutive 16 B)
+    __shared__ u32x4 kqf[2][4][4][2][kDnChunk];
     __shared__ float os[2][kDnChunk][2][kSsmDv];  // scaled recurrence outputs
     // Persistent: workgroup w runs items (sequence, k-head) w, w + G, ...
     // (G = grid size) as one stream of blocks; position q of the stream is
@@ -2548,23 +2587,49 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             }
             const int cur = bb % 3;
             const float(*x)[4 * 128 + 4] = xs[cur];
-            // Phase A: W1 = K S^T and W2 = Q S^T (rows in sigma order)
+            // Phase A: W1 = K S^T and W2 = Q S^T (rows in sigma order) on
+            // fp16 MFMA (v_mfma_f32_16x16x32_f16, 32 k per step in the order
+            // 4 g + e, 16 + 4 g + e of both operands), each operand split
+            // into two fp16 parts after a power-of-two scale: K and Q by 2^14
+            // (entries at most 1 after the normalisation), each state column
+            // so that its largest entry lies in [2^14, 2^15).
             f32x4 w1a[2] = {}, w2a[2] = {};
             {
-                const float* kr = &x[dn_sigma(c)][128 + 4 * g];
-                const float* qr = &x[dn_sigma(c)][4 * g];
+                float ssc[2], sinv[2];
 #pragma unroll
-                for (int m = 0; m < 8; m++) {
-                    const float4 k4 = *reinterpret_cast<const float4*>(kr + 16 * m);
-                    const float4 q4 = *reinterpret_cast<const float4*>(qr + 16 * m);
-                    const float ka[4] = {k4.x, k4.y, k4.z, k4.w}, qa[4] = {q4.x, q4.y, q4.z, q4.w};
+                for (int vt = 0; vt < 2; vt++) {
+                    float mx = 0.f;
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
+                    for (int m = 0; m < 8; m++)
 #pragma unroll
-                        for (int vt = 0; vt < 2; vt++) {
-                            w1a[vt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[e], st[vt][m][e], w1a[vt], 0, 0, 0);
-                            w2a[vt] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[e], st[vt][m][e], w2a[vt], 0, 0, 0);
-                        }
+                        for (int e = 0; e < 4; e++) mx = fmaxf(mx, fabsf(st[vt][m][e]));
+                    mx = fmaxf(mx, __shfl_xor(mx, 16));
+                    mx = fmaxf(mx, __shfl_xor(mx, 32));
+                    const int ex = min(max((int)(__float_as_uint(mx) >> 23), 29), 254);
+                    ssc[vt] = __uint_as_float((uint32_t)(268 - ex) << 23);   // 2^(141 - ex)
+                    sinv[vt] = __uint_as_float((uint32_t)(ex - 28) << 23);   // 2^-14 / ssc
+                }
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    const f16x8_t kh = __builtin_bit_cast(f16x8_t, kqf[0][ks][g][0][c]);
+                    const f16x8_t km = __builtin_bit_cast(f16x8_t, kqf[0][ks][g][1][c]);
+                    const f16x8_t qh = __builtin_bit_cast(f16x8_t, kqf[1][ks][g][0][c]);
+                    const f16x8_t qm = __builtin_bit_cast(f16x8_t, kqf[1][ks][g][1][c]);
+#pragma unroll
+                    for (int vt = 0; vt < 2; vt++) {
+                        const float sv[8] = {st[vt][2 * ks][0],     st[vt][2 * ks][1],     st[vt][2 * ks][2],
+                                             st[vt][2 * ks][3],     st[vt][2 * ks + 1][0], st[vt][2 * ks + 1][1],
+                                             st[vt][2 * ks + 1][2], st[vt][2 * ks + 1][3]};
+                        f16x8_t sh, sm;
+                        dn_split8(sv, ssc[vt], sh, sm);
+                        w1a[vt] = dn_mfma3(kh, km, sh, sm, w1a[vt]);
+                        w2a[vt] = dn_mfma3(qh, qm, sh, sm, w2a[vt]);
+                    }
+                }
+#pragma unroll
+                for (int vt = 0; vt < 2; vt++) {
+                    w1a[vt] *= sinv[vt];
+                    w2a[vt] *= sinv[vt];
                 }
             }
             lds_barrier();
@@ -2800,6 +2865,25 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             for (int i = 0; i < kDnChunk; i++) fc[cur][lane][i] = dn_exp(run - lg[cur][lane][i]);
         }
     };
+    // K and Q of position bb (normalised in place by norm_pass) as fp16
+    // fragments for the state waves' phase A: helper 4 + ks takes 32-k step
+    // ks, lane (row r, group g) the 8 k of that step's lane group g in row r
+    // (sigma order)
+    auto split_pass = [&](int bb) {
+        const float(*x)[4 * 128 + 4] = xs[bb % 3];
+        const int ks = hw - 4;
+        const float* row = &x[dn_sigma(c)][32 * ks + 4 * g];
+#pragma unroll
+        for (int part = 0; part < 2; part++) {
+            const float4 a0 = *reinterpret_cast<const float4*>(row + 128 * (1 - part));
+            const float4 a1 = *reinterpret_cast<const float4*>(row + 128 * (1 - part) + 16);
+            const float v8[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            f16x8_t h, m;
+            dn_split8(v8, 16384.f, h, m);
+            kqf[part][ks][g][0][c] = __builtin_bit_cast(u32x4, h);
+            kqf[part][ks][g][1][c] = __builtin_bit_cast(u32x4, m);
+        }
+    };
     // gated RMSNorm of stream position q's (token, v-head) pairs, 128 dims
     // per wave; pairs past the end or of a position before the first are
     // computed on stale data and their stores discarded
@@ -2857,7 +2941,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 float(*n2)[kDnChunk] = sc[hw][0];
                 float(*n4)[kDnChunk] = sc[hw][1];
                 float(*n8)[kDnChunk] = sc[hw][2];
-                float(*xm)[kDnChunk] = sc[hw][3];
+                float(*xm)[kDnChunk] = sc[hw][0];  // N^2 is dead once X is formed
                 f32x4 pr = dn_m16(n1, n1, g, c);
 #pragma unroll
                 for (int r = 0; r < 4; r++) n2[4 * g + r][c] = pr[r];
@@ -2892,7 +2976,10 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
         // Phase B: K K^T, Q K^T, prefix sums of position bb + 1; conv and
         // gates of position bb + 2 (switching items at a boundary); output
         // norm of position bb - 1
-        if (bb + 1 >= 0 && bb + 1 < n_pos) gram_pass(bb + 1);
+        if (bb + 1 >= 0 && bb + 1 < n_pos) {
+            gram_pass(bb + 1);
+            if (hw >= 4) split_pass(bb + 1);
+        }
         use_x();
         if (bb + 2 < n_pos) {
             if ((bb + 2) % nblk == 0) {
