@@ -2462,6 +2462,41 @@ __device__ __forceinline__ void dn_split8(const float (&x)[8], float s, f16x8_t&
     h = __builtin_bit_cast(f16x8_t, hw);
     m = __builtin_bit_cast(f16x8_t, mw);
 }
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+// dn_split2 with a scale per value (both powers of two, or any positive
+// factors: m = x s - h is then the fp32 rounding of the exact difference)
+__device__ __forceinline__ void dn_split2s(float x0, float x1, float s0, float s1, uint32_t& hp, uint32_t& mp) {
+    uint32_t h;
+    float r0, r1;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]" : "=v"(h) : "v"(x0), "v"(s0));
+    asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel_hi:[0,0,0]" : "+v"(h) : "v"(x1), "v"(s1));
+    asm("v_fma_mix_f32 %0, %1, %2, -%3 op_sel_hi:[0,0,1]" : "=v"(r0) : "v"(x0), "v"(s0), "v"(h));
+    asm("v_fma_mix_f32 %0, %1, %2, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "=v"(r1) : "v"(x1), "v"(s1), "v"(h));
+    hp = h;
+    mp = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(r0, r1));
+}
+__device__ __forceinline__ void dn_split4(const float (&x)[4], const float (&s)[4], f16x4_t& h, f16x4_t& m) {
+    u32x2 hw, mw;
+    uint32_t a, b;
+    dn_split2s(x[0], x[1], s[0], s[1], a, b);
+    hw[0] = a;
+    mw[0] = b;
+    dn_split2s(x[2], x[3], s[2], s[3], a, b);
+    hw[1] = a;
+    mw[1] = b;
+    h = __builtin_bit_cast(f16x4_t, hw);
+    m = __builtin_bit_cast(f16x4_t, mw);
+}
+// largest |entry| of a column held as 4 lane groups x N registers -> the
+// split scale 2^(141 - e) and the inverse of (scale x 2^14), 2^(e - 155), for
+// the column's biased exponent e clamped to [29, 254]
+__device__ __forceinline__ void dn_col_scale(float mx, float& sc, float& inv) {
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const int ex = min(max((int)(__float_as_uint(mx) >> 23), 29), 254);
+    sc = __uint_as_float((uint32_t)(268 - ex) << 23);
+    inv = __uint_as_float((uint32_t)(ex - 28) << 23);
+}
 __device__ __forceinline__ f32x4 dn_mfma3(const f16x8_t& ah, const f16x8_t& am, const f16x8_t& bh,
                                           const f16x8_t& bm, f32x4 acc) {
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(am, bh, acc, 0, 0, 0);
@@ -2660,20 +2695,38 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) os[bb & 1][4 * r + g][hl][i] = o[r] * a.out_scale;
             }
+            // state update on fp16 MFMA (v_mfma_f32_16x16x16_f16: the block's
+            // 16 tokens in one step, lane group g element r = token 4 r + g,
+            // the layout U already has): Kt = diag(fc) K split with the
+            // per-token scale fc 2^14, U per column as the state in phase A;
+            // the product is scaled back and added to e^{g_C} S^T
+            f16x4_t uh[2], um[2];
+            float uinv[2];
 #pragma unroll
-            for (int vt = 0; vt < 2; vt++)
+            for (int vt = 0; vt < 2; vt++) {
+                float usc;
+                dn_col_scale(fmaxf(fmaxf(fabsf(uu[vt][0]), fabsf(uu[vt][1])), fmaxf(fabsf(uu[vt][2]), fabsf(uu[vt][3]))),
+                             usc, uinv[vt]);
+                const float uv[4] = {uu[vt][0], uu[vt][1], uu[vt][2], uu[vt][3]};
+                const float us[4] = {usc, usc, usc, usc};
+                dn_split4(uv, us, uh[vt], um[vt]);
+            }
+            float fcs[4];
 #pragma unroll
-                for (int m = 0; m < 8; m++) st[vt][m] *= egc;
+            for (int r = 0; r < 4; r++) fcs[r] = fc[cur][hl][4 * r + g] * 16384.f;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int tok = 4 * j + g;
-                const float f = fc[cur][hl][tok];
+            for (int m = 0; m < 8; m++) {
+                const float kv[4] = {x[g][128 + 16 * m + c], x[4 + g][128 + 16 * m + c], x[8 + g][128 + 16 * m + c],
+                                     x[12 + g][128 + 16 * m + c]};
+                f16x4_t kh, km;
+                dn_split4(kv, fcs, kh, km);
 #pragma unroll
-                for (int m = 0; m < 8; m++) {
-                    const float ak = f * x[tok][128 + 16 * m + c];
+                for (int vt = 0; vt < 2; vt++) {
+                    f32x4 t = __builtin_amdgcn_mfma_f32_16x16x16f16(km, uh[vt], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, um[vt], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, uh[vt], t, 0, 0, 0);
 #pragma unroll
-                    for (int vt = 0; vt < 2; vt++)
-                        st[vt][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak, uu[vt][j], st[vt][m], 0, 0, 0);
+                    for (int e = 0; e < 4; e++) st[vt][m][e] = fmaf(t[e], uinv[vt], st[vt][m][e] * egc);
                 }
             }
             lds_barrier();
