@@ -2490,12 +2490,13 @@ __device__ __forceinline__ void dn_split4(const float (&x)[4], const float (&s)[
 // largest |entry| of a column held as 4 lane groups x N registers -> the
 // split scale 2^(141 - e) and the inverse of (scale x 2^14), 2^(e - 155), for
 // the column's biased exponent e clamped to [29, 254]
-__device__ __forceinline__ void dn_col_scale(float mx, float& sc, float& inv) {
+__device__ __forceinline__ float dn_col_scale(float mx, float& sc, float& inv) {
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const int ex = min(max((int)(__float_as_uint(mx) >> 23), 29), 254);
     sc = __uint_as_float((uint32_t)(268 - ex) << 23);
     inv = __uint_as_float((uint32_t)(ex - 28) << 23);
+    return mx;
 }
 __device__ __forceinline__ f32x4 dn_mfma3(const f16x8_t& ah, const f16x8_t& am, const f16x8_t& bh,
                                           const f16x8_t& bm, f32x4 acc) {
@@ -2610,7 +2611,26 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 16 * m) = st[vt][m];
             }
         };
+        // smax[vt]: an upper bound of |S^T| over column c of tile vt, exact
+        // after each slice load and carried through the updates as
+        // e^{g_C} smax + 16 max|fc U| (|K| <= 1 after the normalisation, 16
+        // tokens per block); the phase-A split scales come from it.  An
+        // overestimate by 2^k costs the split nothing while k < 17.
+        float smax[2];
+        auto col_max = [&] {
+#pragma unroll
+            for (int vt = 0; vt < 2; vt++) {
+                float mx = 0.f;
+#pragma unroll
+                for (int m = 0; m < 8; m++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) mx = fmaxf(mx, fabsf(st[vt][m][e]));
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                smax[vt] = fmaxf(mx, __shfl_xor(mx, 32));
+            }
+        };
         load_state(slice_of(item_at(0)));
+        col_max();
         lds_barrier();  // positions -2, -1
         lds_barrier();
         lds_barrier();
@@ -2619,6 +2639,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             if (bb > 0 && bb % nblk == 0) {  // next item: this slice out, the next one in
                 store_state(slice_of(item_at(bb - 1)));
                 load_state(slice_of(item_at(bb)));
+                col_max();
             }
             const int cur = bb % 3;
             const float(*x)[4 * 128 + 4] = xs[cur];
@@ -2633,14 +2654,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 float ssc[2], sinv[2];
 #pragma unroll
                 for (int vt = 0; vt < 2; vt++) {
-                    float mx = 0.f;
-#pragma unroll
-                    for (int m = 0; m < 8; m++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++) mx = fmaxf(mx, fabsf(st[vt][m][e]));
-                    mx = fmaxf(mx, __shfl_xor(mx, 16));
-                    mx = fmaxf(mx, __shfl_xor(mx, 32));
-                    const int ex = min(max((int)(__float_as_uint(mx) >> 23), 29), 254);
+                    const int ex = min(max((int)(__float_as_uint(smax[vt]) >> 23), 29), 254);
                     ssc[vt] = __uint_as_float((uint32_t)(268 - ex) << 23);   // 2^(141 - ex)
                     sinv[vt] = __uint_as_float((uint32_t)(ex - 28) << 23);   // 2^-14 / ssc
                 }
@@ -2697,29 +2711,31 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             }
             // state update on fp16 MFMA (v_mfma_f32_16x16x16_f16: the block's
             // 16 tokens in one step, lane group g element r = token 4 r + g,
-            // the layout U already has): Kt = diag(fc) K split with the
-            // per-token scale fc 2^14, U per column as the state in phase A;
+            // the layout U already has): Kt^T U = K^T (diag(fc) U), K^T as
+            // fragments the helpers split in phase A (scale 2^14), diag(fc) U
+            // split per column with the factors fc in the split's multipliers;
             // the product is scaled back and added to e^{g_C} S^T
             f16x4_t uh[2], um[2];
             float uinv[2];
+            float fcv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) fcv[r] = fc[cur][hl][4 * r + g];
 #pragma unroll
             for (int vt = 0; vt < 2; vt++) {
+                const float uv[4] = {uu[vt][0] * fcv[0], uu[vt][1] * fcv[1], uu[vt][2] * fcv[2], uu[vt][3] * fcv[3]};
                 float usc;
-                dn_col_scale(fmaxf(fmaxf(fabsf(uu[vt][0]), fabsf(uu[vt][1])), fmaxf(fabsf(uu[vt][2]), fabsf(uu[vt][3]))),
-                             usc, uinv[vt]);
-                const float uv[4] = {uu[vt][0], uu[vt][1], uu[vt][2], uu[vt][3]};
+                const float mu = dn_col_scale(fmaxf(fmaxf(fabsf(uv[0]), fabsf(uv[1])), fmaxf(fabsf(uv[2]), fabsf(uv[3]))),
+                                              usc, uinv[vt]);
                 const float us[4] = {usc, usc, usc, usc};
                 dn_split4(uv, us, uh[vt], um[vt]);
+                smax[vt] = fmaf(16.f, mu, egc * smax[vt]);
             }
-            float fcs[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) fcs[r] = fc[cur][hl][4 * r + g] * 16384.f;
+            const u32x4* ktf = reinterpret_cast<const u32x4*>(&x[lane >> 5][0]) + (lane & 31);
 #pragma unroll
             for (int m = 0; m < 8; m++) {
-                const float kv[4] = {x[g][128 + 16 * m + c], x[4 + g][128 + 16 * m + c], x[8 + g][128 + 16 * m + c],
-                                     x[12 + g][128 + 16 * m + c]};
-                f16x4_t kh, km;
-                dn_split4(kv, fcs, kh, km);
+                const u32x4 kf = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(ktf) + 2 * m * sizeof(x[0]));
+                const f16x4_t kh = __builtin_bit_cast(f16x4_t, u32x2{kf[0], kf[1]});
+                const f16x4_t km = __builtin_bit_cast(f16x4_t, u32x2{kf[2], kf[3]});
 #pragma unroll
                 for (int vt = 0; vt < 2; vt++) {
                     f32x4 t = __builtin_amdgcn_mfma_f32_16x16x16f16(km, uh[vt], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -2937,6 +2953,26 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             kqf[part][ks][g][1][c] = __builtin_bit_cast(u32x4, m);
         }
     };
+    // K^T of position bb as the state update's fp16 A fragments (scale 2^14):
+    // fragment m (k rows 16 m .. +15) for lane (row c, group g) holds
+    // K[4 r + g][16 m + c], r = 0..3, split into h and m (8 B each).  They go
+    // to the Q columns of the block's own rows, which nothing reads after the
+    // block's gram and split passes: fragment m in rows 2 m (lanes 0..31) and
+    // 2 m + 1 (lanes 32..63).  Helpers 2..5 take fragments 2 (hw - 2) + 0, 1.
+    auto kt_pass = [&](int bb) {
+        float(*x)[4 * 128 + 4] = xs[bb % 3];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int m = 2 * (hw - 2) + i;
+            const float kv[4] = {x[g][128 + 16 * m + c], x[4 + g][128 + 16 * m + c], x[8 + g][128 + 16 * m + c],
+                                 x[12 + g][128 + 16 * m + c]};
+            const float ks[4] = {16384.f, 16384.f, 16384.f, 16384.f};
+            f16x4_t h, mm_;
+            dn_split4(kv, ks, h, mm_);
+            const u32x2 hw2 = __builtin_bit_cast(u32x2, h), mw2 = __builtin_bit_cast(u32x2, mm_);
+            *(reinterpret_cast<u32x4*>(&x[2 * m + (lane >> 5)][0]) + (lane & 31)) = u32x4{hw2[0], hw2[1], mw2[0], mw2[1]};
+        }
+    };
     // gated RMSNorm of stream position q's (token, v-head) pairs, 128 dims
     // per wave; pairs past the end or of a position before the first are
     // computed on stale data and their stores discarded
@@ -3024,6 +3060,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 }
             }
         }
+        if (bb >= 0 && hw >= 2 && hw < 6) kt_pass(bb);
         if (bb + 1 >= 0 && bb + 1 < n_pos) norm_pass(bb + 1);
         lds_barrier();
         // Phase B: K K^T, Q K^T, prefix sums of position bb + 1; conv and
