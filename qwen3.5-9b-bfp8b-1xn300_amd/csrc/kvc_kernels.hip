@@ -2057,7 +2057,8 @@ __device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
 // scalar division is an IEEE divide even in its fast-math build, so beta
 // takes the correctly rounded quotient of sigmoid_ref and matches it bit for
 // bit.  SiLU of the conv output and of z is the AVX-512 form (exp converted
-// to nearest even, :2626, :2714, :3227, :3321), whose fast-math build divides
+// to nearest even, :2626, :2714, :3227, :3321; truncation gives the same
+// SiLU bits, see schraudolph_exp), whose fast-math build divides
 // by an approximate reciprocal: here v_rcp_f32 (1 ulp), so no exact bits
 // exist to match there and the bound is tested against the oracle.  softplus
 // takes log(1 + fast_expf(b)) (:2671, :3278).
@@ -2071,7 +2072,7 @@ __device__ __forceinline__ float dn_beta(float x) {
 template <bool REF>
 __device__ __forceinline__ float dn_silu(float x) {
     if constexpr (REF)
-        return x * __builtin_amdgcn_rcpf(1.0f + schraudolph_exp_rne(0.0f - x));
+        return x * __builtin_amdgcn_rcpf(1.0f + schraudolph_exp(0.0f - x));
     else
         return silu_f(x);
 }
@@ -2603,12 +2604,19 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 for (int m = 0; m < 8; m++) st[vt][m] = *reinterpret_cast<const f32x4*>(src + 16 * m);
             }
         };
+        // The registers hold S^T / dk: the blocks' decays e^{g_C} multiply the
+        // wave-uniform factor dk instead of the 64 state values, so an update
+        // adds its product scaled by 1 / dk with one fma per value.  Once dk
+        // falls below 2^-80 the next update folds it back (S^T dk e^{g_C} +
+        // the product, as without the factor) and dk restarts at 1.  Slices
+        // are stored and loaded in true units.
+        float dk = 1.f;
         auto store_state = [&](float* S) {
 #pragma unroll
             for (int vt = 0; vt < 2; vt++) {
                 float* dst = S + (size_t)(ibase + 16 * vt + c) * kSsmDk + 4 * g;
 #pragma unroll
-                for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 16 * m) = st[vt][m];
+                for (int m = 0; m < 8; m++) *reinterpret_cast<f32x4*>(dst + 16 * m) = st[vt][m] * dk;
             }
         };
         // smax[vt]: an upper bound of |S^T| over column c of tile vt, exact
@@ -2639,6 +2647,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             if (bb > 0 && bb % nblk == 0) {  // next item: this slice out, the next one in
                 store_state(slice_of(item_at(bb - 1)));
                 load_state(slice_of(item_at(bb)));
+                dk = 1.f;
                 col_max();
             }
             const int cur = bb % 3;
@@ -2656,7 +2665,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                 for (int vt = 0; vt < 2; vt++) {
                     const int ex = min(max((int)(__float_as_uint(smax[vt]) >> 23), 29), 254);
                     ssc[vt] = __uint_as_float((uint32_t)(268 - ex) << 23);   // 2^(141 - ex)
-                    sinv[vt] = __uint_as_float((uint32_t)(ex - 28) << 23);   // 2^-14 / ssc
+                    sinv[vt] = __uint_as_float((uint32_t)(ex - 28) << 23) * dk;  // dk 2^-14 / ssc
                 }
 #pragma unroll
                 for (int ks = 0; ks < 4; ks++) {
@@ -2684,7 +2693,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             lds_barrier();
             // Phase B: U = T diag(beta) (V - diag(e^g) W1); O = diag(e^g) W2 + M U;
             // S^T <- e^{g_C} S^T + Kt^T U.  Lane group g, register r <-> token 4 r + g.
-            const float egc = eg[cur][hl][kDnChunk - 1];
+            const float egc = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(eg[cur][hl][kDnChunk - 1])));  // uniform
             f32x4 uu[2];
 #pragma unroll
             for (int vt = 0; vt < 2; vt++) {
@@ -2718,6 +2727,9 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
             f16x4_t uh[2], um[2];
             float uinv[2];
             float fcv[4];
+            const float dkn = dk * egc;
+            const bool fold = !(dkn >= 0x1p-80f);  // uniform
+            const float rdk = fold ? 1.f : 1.f / dkn;
 #pragma unroll
             for (int r = 0; r < 4; r++) fcv[r] = fc[cur][hl][4 * r + g];
 #pragma unroll
@@ -2728,9 +2740,17 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                                               usc, uinv[vt]);
                 const float us[4] = {usc, usc, usc, usc};
                 dn_split4(uv, us, uh[vt], um[vt]);
-                smax[vt] = fmaf(16.f, mu, egc * smax[vt]);
+                smax[vt] = fold ? fmaf(16.f, mu, dkn * smax[vt]) : fmaf(16.f * mu, rdk, smax[vt]);
+                uinv[vt] *= rdk;
             }
             const u32x4* ktf = reinterpret_cast<const u32x4*>(&x[lane >> 5][0]) + (lane & 31);
+            if (fold) {  // uniform
+#pragma unroll
+                for (int vt = 0; vt < 2; vt++)
+#pragma unroll
+                    for (int m = 0; m < 8; m++) st[vt][m] *= dkn;
+            }
+            dk = fold ? 1.f : dkn;
 #pragma unroll
             for (int m = 0; m < 8; m++) {
                 const u32x4 kf = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(ktf) + 2 * m * sizeof(x[0]));
@@ -2742,7 +2762,7 @@ void deltanet_mfma_kernel(DeltaNetArgs a) {
                     t = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, um[vt], t, 0, 0, 0);
                     t = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, uh[vt], t, 0, 0, 0);
 #pragma unroll
-                    for (int e = 0; e < 4; e++) st[vt][m][e] = fmaf(t[e], uinv[vt], st[vt][m][e] * egc);
+                    for (int e = 0; e < 4; e++) st[vt][m][e] = fmaf(t[e], uinv[vt], st[vt][m][e]);
                 }
             }
             lds_barrier();
