@@ -342,7 +342,7 @@ def run_b(args):
     B.close()
     sweep = None
     floor_checksum_us = floor_us
-    if "floor" in legs:
+    if "floor" in legs and not getattr(args, "no_floor_sweep", False):
         log("b leg floor sweep (libkvc_calib.so)")
         sweep = read_floor_sweep()
         if sweep is not None:
@@ -1169,6 +1169,10 @@ def main():
                     help="config b: comma list of the legs to run (decode = the headline launch, floor, "
                          "two_launch, fused = the attention step modes)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-floor-sweep", action="store_true",
+                    help="config b: time the floor with the checksum leg only, without libkvc_calib.so's "
+                         "launch-shape sweep (its 64 capture / destroy cycles crash rocprofv3's library, "
+                         "so profiled runs leave it out)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--phases", action="store_true",
                     help="config b's decode launch with phase stamps (libkvc_phases.so); prints the phase table")
