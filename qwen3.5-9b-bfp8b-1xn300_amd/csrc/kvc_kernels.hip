@@ -2427,10 +2427,10 @@ void deltanet_kernel(DeltaNetArgs a) {
 // and log decay 0, which leaves U, O and S unchanged.
 constexpr int kDnChunk = 16;
 // Calls of this many tokens or more run the matrix form (one partial block
-// below 16).  Measured at config e (64 sessions): the blocked kernel takes
-// 84 / 97 us per layer at 12 / 15 tokens, the matrix form 91.5 / 92.2; the two
-// meet at 14.
-constexpr int kDnMatrixMin = 14;
+// below 16).  Measured at config e (64 sessions, interleaved): the blocked
+// kernel takes 84.0-85.4 / 89.9-90.2 us per layer at 12 / 13 tokens, the
+// matrix form 86.8 / 86.9-87.1; the two meet between 12 and 13.
+constexpr int kDnMatrixMin = 13;
 static_assert(kDnMatrixMin <= 2 * kDnBlk, "the blocked kernel covers calls of at most two blocks");
 
 __device__ __forceinline__ int dn_sigma(int r) { return 4 * (r & 3) + (r >> 2); }

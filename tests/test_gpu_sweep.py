@@ -197,8 +197,8 @@ def test_decode_loop_across_blocks(chunk):
             assert np.array_equal(got[i][0], mk) and np.array_equal(got[i][1], mv), s
 
 
-# Gated-DeltaNet step: token counts across the blocked kernel (2..13, one and
-# two blocks) and the matrix form (14 and more, partial last blocks), with
+# Gated-DeltaNet step: token counts across the blocked kernel (2..12, one and
+# two blocks) and the matrix form (13 and more, partial last blocks), with
 # every pairing of input and output dtype and both math modes; the state, the
 # conv window and every token's output are checked against the oracle
 # (run_case of test_gpu_deltanet).
@@ -207,6 +207,7 @@ DN_CASES = [
     (6, kvc.DTYPE_BF16, kvc.DTYPE_BF16, 4, True),
     (11, kvc.DTYPE_F32, kvc.DTYPE_F32, 3, False),
     (12, kvc.DTYPE_BF16, kvc.DTYPE_BF16, 6, False),
+    (13, kvc.DTYPE_BF16, kvc.DTYPE_F32, 3, True),
     (15, kvc.DTYPE_F32, kvc.DTYPE_BF16, 2, True),
     (17, kvc.DTYPE_BF16, kvc.DTYPE_F32, 3, False),
     (31, kvc.DTYPE_F32, kvc.DTYPE_F32, 2, False),
